@@ -1,0 +1,178 @@
+/*
+ * qwen_w4a16.h -- C-ABI of the MI355X (gfx950) W4A16 quantized-matmul path.
+ *
+ * Plain C: device pointers, sizes and status codes only. `stream` is a
+ * hipStream_t passed as void* (NULL = the null stream). Every call that
+ * launches work is asynchronous on that stream, never synchronizes and never
+ * allocates, so it can be captured into a hipGraph; the *_alloc / *_free calls
+ * are the only ones that allocate or free.
+ *
+ * Each entry point names the reference interface it replaces
+ * (patrickbdevaney/qwen38-3090-cuda-server, path:line). The reference aborts on
+ * bad input; these return a status code instead, and the C++ layer in
+ * qwen_w4a16.hpp turns a non-zero code into a message plus abort() so existing
+ * reference callers keep their behaviour.
+ *
+ * Weight format accepted: INT4, asymmetric, group 128, stored nibbles 0..15
+ * (w = (q - zp) * scale). Shapes: out_f % 64 == 0, in_f % 512 == 0.
+ */
+#ifndef QWEN_W4A16_H
+#define QWEN_W4A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------ status */
+enum {
+  QW4_OK = 0,
+  QW4_ERR_NULL = 1,        /* a required pointer is NULL                         */
+  QW4_ERR_SHAPE = 2,       /* out_f % 64, in_f % 512, row offset or M invalid    */
+  QW4_ERR_GROUP = 3,       /* group_size other than 128                          */
+  QW4_ERR_M = 4,           /* M outside the range the entry point supports       */
+  QW4_ERR_SCRATCH = 5,     /* scratch / workspace too small for this call        */
+  QW4_ERR_ALIGN = 6,       /* activation / output pointer not 16-byte aligned    */
+  QW4_ERR_HIP = 7,         /* a HIP runtime call failed (see qw4_last_hip_error)  */
+  QW4_ERR_NOMEM = 8,       /* device allocation failed                           */
+  QW4_ERR_LAYOUT = 9       /* unknown source layout id                           */
+};
+
+const char* qw4_status_string(int status);
+int qw4_last_hip_error(void);   /* hipError_t of the last QW4_ERR_HIP, this thread */
+int qw4_version(void);
+
+/* ------------------------------------------------------------- weights
+ * Device-resident repacked weights (the reference's W4A16Weights,
+ * src/kernels/gemv_w4a16.cuh:50-60). The internal layout is private to the
+ * library; its three buffers are separate allocations, each freeable with
+ * hipFree, as the reference's callers do (src/model/model.cu:111, :204).
+ */
+typedef struct qw4_weights {
+  uint32_t* qweight;   /* packed nibbles, tile-major                   */
+  uint16_t* scale;     /* bf16, per (row, group)                        */
+  uint16_t* zeros;     /* 4-bit zero points, 4 rows per u16             */
+  int32_t out_f, in_f, group_size, num_groups;
+} qw4_weights;
+
+size_t qw4_weights_bytes(const qw4_weights* w);   /* device bytes held */
+
+/* awq_alloc_fused (src/kernels/gemv_w4a16.cuh:81-82; .cu:308-315). */
+int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void* stream);
+/* awq_free (gemv_w4a16.cuh:86; .cu:331-334). */
+int qw4_weights_free(qw4_weights* w);
+
+/* awq_repack_into (gemv_w4a16.cuh:83-85; .cu:317-323): compressed-tensors
+ * pack-quantized source (src/loader/w4a16_unpack.h:1-18)
+ *   packed [out_f][in_f/8] u32, scale [out_f][G] bf16, zp [out_f/8][G] u32,
+ * written at destination rows [row_offset, row_offset + out_f) (row_offset % 64 == 0). */
+int qw4_repack_ct_into(qw4_weights* w, int row_offset, const uint32_t* packed,
+                       const uint16_t* scale, const uint32_t* zp, int out_f, void* stream);
+/* awq_repack (gemv_w4a16.cuh:70-75; .cu:325-329) = alloc + repack_into(0). */
+int qw4_repack_ct(qw4_weights* w, const uint32_t* packed, const uint16_t* scale,
+                  const uint32_t* zp, int out_f, int in_f, int group_size, void* stream);
+
+/* AWQ-order sources (no reference counterpart: the benchmark's input format).
+ *   QW4_LAYOUT_AWQ_K: qweight [in_f/8][out_f] u32 packed along K,
+ *   QW4_LAYOUT_AWQ_N: qweight [in_f][out_f/8] u32 packed along N (AutoAWQ GEMM),
+ * both with nibble order {0,2,4,6,1,3,5,7}, scales [G][out_f] bf16 and
+ * zeros [G][out_f/8] u32 in the same nibble order along N. */
+enum { QW4_LAYOUT_AWQ_K = 1, QW4_LAYOUT_AWQ_N = 2 };
+int qw4_repack_awq_into(qw4_weights* w, int row_offset, const uint32_t* qweight,
+                        const uint16_t* scales, const uint32_t* zeros, int out_f,
+                        int layout, void* stream);
+
+/* w4a16_dequant_rows (src/kernels/gemm_w4a16.cuh:45-48; .cu:56-61):
+ * dst [nrows][in_f] bf16 row-major = RNE((q - zp) * s) for rows row0.. */
+int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows,
+                     void* stream);
+
+/* ------------------------------------------------------------- scratch
+ * GemvScratch (gemv_w4a16.cuh:94-110): split-K partials and the self-resetting
+ * counters of the skinny kernels. Counters start at zero and every call leaves
+ * them at zero, so calls may be graph-captured; two calls that share one
+ * scratch must not run concurrently.
+ */
+typedef struct qw4_scratch {
+  float* partial;          /* split-K partials                               */
+  uint32_t* counters;      /* per-tile arrival counters (+1 argmax counter)  */
+  uint64_t* keys;          /* argmax keys, one per row                       */
+  size_t partial_elems;
+  int32_t max_in, max_out, max_m, max_tiles;
+} qw4_scratch;
+
+/* gemv_scratch_alloc (gemv_w4a16.cuh:106-107; .cu:344-355). */
+int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, int max_m);
+/* gemv_scratch_free (gemv_w4a16.cuh:108; .cu:368-371). */
+int qw4_scratch_free(qw4_scratch* s);
+/* gemv_partial_check (gemv_w4a16.cuh:109-110; .cu:359-366), as a status code. */
+int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
+/* gemv_choose_splits (gemv_w4a16.cuh:134; .cu:289-306): K-splits the skinny
+ * kernel uses for this shape (env QW4_SKINNY_WGS overrides the target). */
+int qw4_choose_splits(int out_f, int num_groups);
+
+/* ------------------------------------------------------- decode / verify
+ * y [M][out_f] = x [M][in_f] @ W^T, bf16 row-major, fp32 accumulation.
+ * x must be 16-byte aligned; y 8-byte aligned (16 for fp32).
+ */
+/* gemv_w4a16 (gemv_w4a16.cuh:130-131; .cu:464-469), M = 1. */
+int qw4_gemv(uint16_t* y, const qw4_weights* w, const uint16_t* x, qw4_scratch* s,
+             void* stream);
+/* gemv_w4a16_f32 (gemv_w4a16.cuh:132-133; .cu:456-462), M = 1, fp32 output. */
+int qw4_gemv_f32(float* y, const qw4_weights* w, const uint16_t* x, qw4_scratch* s,
+                 void* stream);
+/* gemm_small_w4a16 (gemv_w4a16.cuh:124-125; .cu:396-454), 1 <= M <= 16. */
+int qw4_gemm_small(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
+                   qw4_scratch* s, void* stream);
+/* gemm_mma_w4a16 (gemv_w4a16.cuh:187-188; .cu:842-865), 1 <= M <= 16. */
+int qw4_gemm_mma(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
+                 qw4_scratch* s, void* stream);
+
+/* lm_head GEMV fused with an fp32 row-argmax (lowest index on ties). Replaces
+ * head() + argmax / model_apply_head() + argmax_rows (src/model/model.cu:796-815,
+ * :1009-1051; src/kernels/elementwise.cuh:39-43) without writing logits.
+ * idx [M] int32, 1 <= M <= 16. */
+int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
+                    qw4_scratch* s, void* stream);
+
+/* ------------------------------------------------------------- prefill
+ * GemmWorkspace (src/kernels/gemm_w4a16.cuh:30-35). The fused kernel needs
+ * only split-K partials; bytes may be 0 (then split-K is disabled). */
+typedef struct qw4_workspace {
+  void* buf;
+  size_t bytes;
+} qw4_workspace;
+
+/* gemm_workspace_alloc / _free (gemm_w4a16.cuh:37-38; .cu:42-54). */
+int qw4_workspace_alloc(qw4_workspace* ws, size_t bytes);
+int qw4_workspace_free(qw4_workspace* ws);
+/* gemm_w4a16 (gemm_w4a16.cuh:40-43; .cu:63-88): C [M][out_f] bf16 =
+ * A [M][in_f] bf16 @ W^T with W dequantized to bf16 (RNE((q-zp)*s)), bf16 MFMA,
+ * fp32 accumulation. Any M >= 1. */
+int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M,
+             qw4_workspace* ws, void* stream);
+
+/* -------------------------------------------------------------- argmax
+ * argmax / argmax_rows over bf16 logits (src/kernels/elementwise.cuh:34-43;
+ * .cu:96-158, :184-194), lowest index on ties. argmax's scratch holds
+ * >= 512 int32 (the reference's 256 (idx, val) pairs). */
+int qw4_argmax(int32_t* out, const uint16_t* x, int n, int32_t* scratch, void* stream);
+int qw4_argmax_rows(int32_t* out, const uint16_t* x, int rows, int n, void* stream);
+
+/* ------------------------------------------------- synthetic inputs
+ * Device-side generator for the benchmark (no reference counterpart). The
+ * counter-based spec is documented with the generator kernel:
+ *   kind 0: x = bf16(N(0,1)), kind 1: scale = bf16(|N(0,0.02)| + 1e-4).
+ * qw4_gen_awq_k writes one tensor in QW4_LAYOUT_AWQ_K form from streams
+ * tensor*8 + {0: q, 1: zp, 2: scale}. */
+int qw4_gen_bf16(uint16_t* out, size_t count, uint64_t seed, uint64_t stream_id,
+                 uint64_t offset, int kind, void* stream);
+int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_f,
+                  int in_f, uint64_t seed, uint64_t tensor, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QWEN_W4A16_H */

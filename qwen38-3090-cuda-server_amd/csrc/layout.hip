@@ -1,0 +1,364 @@
+// Load-time side of the library: weight allocation, the repack from the three
+// accepted source layouts into the tile-major layout (w4a16_common.h), the
+// bf16 dequant of repacked rows, status strings and the synthetic generator.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/qwen_w4a16.h"
+#include "w4a16_common.h"
+
+namespace qw4 {
+
+static thread_local int g_last_hip_error = 0;
+void set_hip_error(int e) { g_last_hip_error = e; }
+
+namespace {
+
+// Nibble slot of element e in the AWQ order {0,2,4,6,1,3,5,7}: slot i holds
+// element AWQ_ORDER[i], so element e sits at slot (e % 2) * 4 + e / 2 -- the same
+// slot order as the repacked layout, which is why AWQ words along K move as is.
+__device__ __forceinline__ int awq_slot(int e) { return slot_of_elem(e); }
+
+// ------------------------------------------------------------------ repack
+// One thread per destination word. Source layouts:
+//   0 = compressed-tensors [N][K/8] (element e at slot e; w4a16_unpack.h:25-29)
+//   1 = AWQ packed along K [K/8][N], 2 = AWQ packed along N [K][N/8].
+template <int SRC>
+__global__ void k_repack_q(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src,
+                           int n_src, int K, int G, int tile0) {
+  const size_t per_tile = (size_t)G * kWordsPerBlock;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)(n_src / kTileN) * per_tile) return;
+  const int bl = (int)(t / per_tile);
+  const int rem = (int)(t % per_tile);
+  const int g = rem >> 10, j = (rem >> 8) & 3, p = (rem >> 2) & 63, w = rem & 3;
+  const int ns = bl * kTileN + tile_row_of_pos(p);     // source row
+  const int r = g * 16 + 4 * j + w;                    // word of the row: k = 8r..8r+7
+  uint32_t out = 0;
+  if (SRC == 0) {
+    const uint32_t s = src[(size_t)ns * (K / 8) + r];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out |= ((s >> (4 * e)) & 0xFu) << (4 * slot_of_elem(e));
+  } else if (SRC == 1) {
+    const uint32_t s = src[(size_t)r * n_src + ns];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out |= ((s >> (4 * awq_slot(e))) & 0xFu) << (4 * slot_of_elem(e));
+  } else {
+    const int sh = 4 * awq_slot(ns & 7);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t s = src[(size_t)(8 * r + e) * (n_src / 8) + (ns >> 3)];
+      out |= ((s >> sh) & 0xFu) << (4 * slot_of_elem(e));
+    }
+  }
+  dst[(size_t)(tile0 + bl) * per_tile + rem] = out;
+}
+
+// One thread per (tile, group, 4-row quad): scales and zero points.
+template <int SRC>
+__global__ void k_repack_meta(uint16_t* __restrict__ dscale, uint16_t* __restrict__ dzero,
+                              const uint16_t* __restrict__ sscale,
+                              const uint32_t* __restrict__ szero, int n_src, int G,
+                              int tile0) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (n_src / kTileN) * G * 16) return;
+  const int bl = t / (G * 16), g = (t / 16) % G, c = t & 15;
+  const size_t blk = (size_t)(tile0 + bl) * G + g;
+  uint32_t z = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ns = bl * kTileN + 4 * c + i;
+    uint16_t s;
+    uint32_t zn;
+    if (SRC == 0) {
+      s = sscale[(size_t)ns * G + g];
+      zn = (szero[(size_t)(ns >> 3) * G + g] >> (4 * (ns & 7))) & 0xFu;  // w4a16_unpack.h:38-42
+    } else {
+      s = sscale[(size_t)g * n_src + ns];
+      zn = (szero[(size_t)g * (n_src / 8) + (ns >> 3)] >> (4 * awq_slot(ns & 7))) & 0xFu;
+    }
+    dscale[blk * 64 + 4 * c + i] = s;
+    z |= zn << (4 * i);
+  }
+  dzero[blk * 16 + c] = (uint16_t)z;
+}
+
+// ----------------------------------------------------------------- dequant
+// dst [nrows][K] = RNE(float(q - z) * s), one thread per 8 consecutive k.
+__global__ void k_dequant_rows(uint16_t* __restrict__ dst, const uint32_t* __restrict__ qw,
+                               const uint16_t* __restrict__ sc,
+                               const uint16_t* __restrict__ zr, int row0, int nrows,
+                               int K, int G) {
+  const int wpr = K / 8;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)nrows * wpr) return;
+  const int r = (int)(t / wpr), wi = (int)(t % wpr);
+  const int n = row0 + r, b = n >> 6, rr = n & 63;
+  const int g = wi >> 4, j = (wi >> 2) & 3, w = wi & 3;
+  const size_t blk = (size_t)b * G + g;
+  const uint32_t word = qw[blk * kWordsPerBlock + j * 256 + tile_pos_of_row(rr) * 4 + w];
+  const float s = bf16_bits_to_f32(sc[blk * 64 + rr]);
+  const int z = (zr[blk * 16 + (rr >> 2)] >> (4 * (rr & 3))) & 0xF;
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const float a = (float)((int)((word >> (4 * slot_of_elem(e))) & 0xFu) - z) * s;
+    const float c = (float)((int)((word >> (4 * slot_of_elem(e + 1))) & 0xFu) - z) * s;
+    o[e / 2] = pack_bf16x2(a, c);
+  }
+  *reinterpret_cast<u32x4*>(dst + (size_t)r * K + 8 * wi) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
+// --------------------------------------------------------------- generator
+// Counter-based synthetic inputs (identical spec in the CPU test oracle):
+//   key = mix64(seed * 0xD1B54A32D192ED03 + stream_id)
+//   draw(i) = mix64(key + (i + 1) * 0x9E3779B97F4A7C15), mix64 = SplitMix64 finalizer
+//   u4(i) = draw(i) >> 60
+//   normal(i) = Irwin-Hall(12) of the 16-bit fields of draw(3i..3i+2):
+//               (S + 6) / 65536 - 6, exact in fp32
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+__device__ __forceinline__ uint64_t gkey(uint64_t seed, uint64_t stream) {
+  return mix64(seed * 0xD1B54A32D192ED03ull + stream);
+}
+__device__ __forceinline__ uint64_t gdraw(uint64_t key, uint64_t i) {
+  return mix64(key + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+__device__ __forceinline__ float gnormal(uint64_t key, uint64_t i) {
+  uint32_t s = 0;
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    const uint64_t r = gdraw(key, 3 * i + t);
+    s += (uint32_t)(r & 0xffff) + (uint32_t)((r >> 16) & 0xffff) +
+         (uint32_t)((r >> 32) & 0xffff) + (uint32_t)(r >> 48);
+  }
+  return __fsub_rn(__fmul_rn(__fadd_rn((float)s, 6.0f), 1.0f / 65536.0f), 6.0f);
+}
+__device__ __forceinline__ uint16_t rne_bf16(float f) {
+  const uint32_t u = __float_as_uint(f);
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ uint16_t gen_value(uint64_t key, uint64_t i, int kind) {
+  const float v = gnormal(key, i);
+  return kind == 0 ? rne_bf16(v) : rne_bf16(__fadd_rn(fabsf(__fmul_rn(v, 0.02f)), 1e-4f));
+}
+
+__global__ void k_gen_bf16(uint16_t* out, size_t count, uint64_t seed, uint64_t stream,
+                           uint64_t offset, int kind) {
+  const uint64_t key = gkey(seed, stream);
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (size_t)gridDim.x * blockDim.x)
+    out[i] = gen_value(key, offset + i, kind);
+}
+
+// qweight [K/8][N]: slot i of word [r][n] <- q[n][8r + AWQ_ORDER[i]], q[n][k] = u4(n*K + k)
+__global__ void k_gen_awq_k_q(uint32_t* qw, int N, int K, uint64_t seed, uint64_t tensor) {
+  const uint64_t key = gkey(seed, tensor * 8 + 0);
+  const size_t total = (size_t)(K / 8) * N;
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (size_t)gridDim.x * blockDim.x) {
+    const size_t r = t / N, n = t % N;
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t q = (uint32_t)(gdraw(key, n * (size_t)K + 8 * r + e) >> 60);
+      w |= q << (4 * awq_slot(e));
+    }
+    qw[t] = w;
+  }
+}
+
+// scales [G][N] bf16 (s[n][g] = scale(n*G + g)); zeros [G][N/8] (zp[n][g] = u4(n*G + g))
+__global__ void k_gen_awq_k_meta(uint16_t* sc, uint32_t* zr, int N, int G, uint64_t seed,
+                                 uint64_t tensor) {
+  const uint64_t kz = gkey(seed, tensor * 8 + 1), ks = gkey(seed, tensor * 8 + 2);
+  const size_t total = (size_t)G * (N / 8);
+  for (size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x; t < total;
+       t += (size_t)gridDim.x * blockDim.x) {
+    const size_t g = t / (N / 8), c = t % (N / 8);
+    uint32_t w = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const size_t n = 8 * c + e;
+      w |= (uint32_t)(gdraw(kz, n * G + g) >> 60) << (4 * awq_slot(e));
+      sc[g * N + n] = gen_value(ks, n * G + g, 1);
+    }
+    zr[t] = w;
+  }
+}
+
+int check_weights(const qw4_weights* w) {
+  if (!w || !w->qweight || !w->scale || !w->zeros) return QW4_ERR_NULL;
+  if (w->group_size != kGroup) return QW4_ERR_GROUP;
+  if (w->out_f <= 0 || w->out_f % kTileN || w->in_f <= 0 || w->in_f % 512 ||
+      w->num_groups != w->in_f / kGroup)
+    return QW4_ERR_SHAPE;
+  return QW4_OK;
+}
+
+unsigned blocks_for(size_t n, unsigned tpb) { return (unsigned)((n + tpb - 1) / tpb); }
+
+}  // namespace
+
+int check_weights_public(const qw4_weights* w) { return check_weights(w); }
+
+}  // namespace qw4
+
+using namespace qw4;
+
+extern "C" {
+
+const char* qw4_status_string(int st) {
+  switch (st) {
+    case QW4_OK: return "ok";
+    case QW4_ERR_NULL: return "null pointer";
+    case QW4_ERR_SHAPE: return "unsupported shape (out_f % 64, in_f % 512, row offset or size)";
+    case QW4_ERR_GROUP: return "unsupported group size (only 128)";
+    case QW4_ERR_M: return "M out of range for this entry point";
+    case QW4_ERR_SCRATCH: return "scratch or workspace too small";
+    case QW4_ERR_ALIGN: return "pointer not aligned (16 bytes for activations)";
+    case QW4_ERR_HIP: return "HIP runtime error";
+    case QW4_ERR_NOMEM: return "device allocation failed";
+    case QW4_ERR_LAYOUT: return "unknown source layout";
+    default: return "unknown status";
+  }
+}
+
+int qw4_last_hip_error(void) { return g_last_hip_error; }
+int qw4_version(void) { return 1; }
+
+size_t qw4_weights_bytes(const qw4_weights* w) {
+  if (!w) return 0;
+  const size_t n = (size_t)w->out_f, k = (size_t)w->in_f, g = (size_t)w->num_groups;
+  return n * k / 2 + n * g * 2 + n * g / 2;
+}
+
+int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void* stream) {
+  (void)stream;
+  if (!w) return QW4_ERR_NULL;
+  if (group_size != kGroup) return QW4_ERR_GROUP;
+  if (out_f <= 0 || out_f % kTileN || in_f <= 0 || in_f % 512) return QW4_ERR_SHAPE;
+  std::memset(w, 0, sizeof(*w));
+  w->out_f = out_f;
+  w->in_f = in_f;
+  w->group_size = group_size;
+  w->num_groups = in_f / group_size;
+  const size_t n = (size_t)out_f, g = (size_t)w->num_groups;
+  hipError_t e = hipMalloc((void**)&w->qweight, n * in_f / 2);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->scale, n * g * 2);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->zeros, n * g / 2);
+  if (e != hipSuccess) {
+    set_hip_error((int)e);
+    (void)hipGetLastError();
+    qw4_weights_free(w);
+    return QW4_ERR_NOMEM;
+  }
+  return QW4_OK;
+}
+
+int qw4_weights_free(qw4_weights* w) {
+  if (!w) return QW4_ERR_NULL;
+  if (w->qweight) (void)hipFree(w->qweight);
+  if (w->scale) (void)hipFree(w->scale);
+  if (w->zeros) (void)hipFree(w->zeros);
+  std::memset(w, 0, sizeof(*w));
+  return QW4_OK;
+}
+
+static int repack_into(qw4_weights* w, int row_offset, const uint32_t* q, const uint16_t* s,
+                       const uint32_t* z, int out_f, int src, void* stream) {
+  int st = check_weights(w);
+  if (st) return st;
+  if (!q || !s || !z) return QW4_ERR_NULL;
+  if (out_f <= 0 || out_f % kTileN || row_offset < 0 || row_offset % kTileN ||
+      row_offset + out_f > w->out_f)
+    return QW4_ERR_SHAPE;
+  hipStream_t hs = (hipStream_t)stream;
+  const int G = w->num_groups, tile0 = row_offset / kTileN;
+  const size_t nq = (size_t)(out_f / kTileN) * G * kWordsPerBlock;
+  const size_t nm = (size_t)(out_f / kTileN) * G * 16;
+  switch (src) {
+    case 0:
+      k_repack_q<0><<<blocks_for(nq, 256), 256, 0, hs>>>(w->qweight, q, out_f, w->in_f, G, tile0);
+      k_repack_meta<0><<<blocks_for(nm, 256), 256, 0, hs>>>(w->scale, w->zeros, s, z, out_f, G, tile0);
+      break;
+    case QW4_LAYOUT_AWQ_K:
+      k_repack_q<1><<<blocks_for(nq, 256), 256, 0, hs>>>(w->qweight, q, out_f, w->in_f, G, tile0);
+      k_repack_meta<1><<<blocks_for(nm, 256), 256, 0, hs>>>(w->scale, w->zeros, s, z, out_f, G, tile0);
+      break;
+    case QW4_LAYOUT_AWQ_N:
+      k_repack_q<2><<<blocks_for(nq, 256), 256, 0, hs>>>(w->qweight, q, out_f, w->in_f, G, tile0);
+      k_repack_meta<1><<<blocks_for(nm, 256), 256, 0, hs>>>(w->scale, w->zeros, s, z, out_f, G, tile0);
+      break;
+    default:
+      return QW4_ERR_LAYOUT;
+  }
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_repack_ct_into(qw4_weights* w, int row_offset, const uint32_t* packed,
+                       const uint16_t* scale, const uint32_t* zp, int out_f, void* stream) {
+  return repack_into(w, row_offset, packed, scale, zp, out_f, 0, stream);
+}
+
+int qw4_repack_ct(qw4_weights* w, const uint32_t* packed, const uint16_t* scale,
+                  const uint32_t* zp, int out_f, int in_f, int group_size, void* stream) {
+  int st = qw4_weights_alloc(w, out_f, in_f, group_size, stream);
+  if (st) return st;
+  return repack_into(w, 0, packed, scale, zp, out_f, 0, stream);
+}
+
+int qw4_repack_awq_into(qw4_weights* w, int row_offset, const uint32_t* qweight,
+                        const uint16_t* scales, const uint32_t* zeros, int out_f, int layout,
+                        void* stream) {
+  if (layout != QW4_LAYOUT_AWQ_K && layout != QW4_LAYOUT_AWQ_N) return QW4_ERR_LAYOUT;
+  return repack_into(w, row_offset, qweight, scales, zeros, out_f, layout, stream);
+}
+
+int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows, void* stream) {
+  int st = check_weights(w);
+  if (st) return st;
+  if (!dst) return QW4_ERR_NULL;
+  if (row0 < 0 || nrows < 0 || row0 + nrows > w->out_f) return QW4_ERR_SHAPE;
+  if (((uintptr_t)dst & 15) != 0) return QW4_ERR_ALIGN;
+  if (nrows == 0) return QW4_OK;
+  const size_t n = (size_t)nrows * (w->in_f / 8);
+  k_dequant_rows<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
+      dst, w->qweight, w->scale, w->zeros, row0, nrows, w->in_f, w->num_groups);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_gen_bf16(uint16_t* out, size_t count, uint64_t seed, uint64_t stream_id,
+                 uint64_t offset, int kind, void* stream) {
+  if (!out) return QW4_ERR_NULL;
+  if (count == 0) return QW4_OK;
+  const unsigned nb = (unsigned)std::min<size_t>(blocks_for(count, 256), 65536);
+  k_gen_bf16<<<nb, 256, 0, (hipStream_t)stream>>>(out, count, seed, stream_id, offset, kind);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_f, int in_f,
+                  uint64_t seed, uint64_t tensor, void* stream) {
+  if (!qweight || !scales || !zeros) return QW4_ERR_NULL;
+  if (out_f <= 0 || out_f % 8 || in_f <= 0 || in_f % kGroup) return QW4_ERR_SHAPE;
+  hipStream_t hs = (hipStream_t)stream;
+  const size_t nq = (size_t)(in_f / 8) * out_f;
+  k_gen_awq_k_q<<<(unsigned)std::min<size_t>(blocks_for(nq, 256), 65536), 256, 0, hs>>>(
+      qweight, out_f, in_f, seed, tensor);
+  const size_t nm = (size_t)(in_f / kGroup) * (out_f / 8);
+  k_gen_awq_k_meta<<<(unsigned)std::min<size_t>(blocks_for(nm, 256), 65536), 256, 0, hs>>>(
+      scales, zeros, out_f, in_f / kGroup, seed, tensor);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+}  // extern "C"

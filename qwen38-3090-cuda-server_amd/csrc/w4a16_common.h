@@ -1,0 +1,90 @@
+// Shared definitions of the gfx950 W4A16 library: the repacked weight layout,
+// vector types and the nibble -> bf16 conversion every kernel uses.
+//
+// Repacked layout (one "tile" = 64 output rows, one "group" = 128 inputs):
+//
+//   qweight u32 [N/64][G][4 j][64 p][4 w]          (4 KiB per (tile, group))
+//       position p of a tile holds row  n = 4*(p % 16) + p / 16,
+//       word w of chunk j covers k = 128*g + 32*j + 8*w + e, e = 0..7,
+//       element e sits in nibble slot (e % 2) * 4 + e / 2.
+//   scale   bf16 [N/64][G][64]        natural row order inside the tile
+//   zeros   u16  [N/64][G][16]        u16 c holds rows 4c..4c+3, row 4c+t at bits 4t
+//
+// Why this shape:
+//   * nibble slot order: ((w >> 4p) & 0x000F000F) | 0x43004300 is the bf16 pair
+//     (128 + q[2p], 128 + q[2p+1]) -- exact, since bf16 has ulp 1 on [128, 256) --
+//     so four AND-OR operations (three after shifts) turn one word into the 8
+//     consecutive-k bf16 operand of an MFMA, with no activation permutation.
+//   * position order: a wave loading 16-byte chunk j of positions 16*st + c
+//     (c = lane % 16) reads 256 contiguous bytes and gets rows 4c + st, so after
+//     the four st loads each lane owns four consecutive rows: its scales are one
+//     8-byte load, its zero points one u16, its outputs one 8-byte store.
+//   * the (tile, group) block is 4 KiB contiguous: the decode kernels stream
+//     it with 16-byte loads and the prefill GEMM stages it into LDS unchanged.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qw4 {
+
+constexpr int kTileN = 64;          // output rows per tile
+constexpr int kGroup = 128;         // inputs per quantization group
+constexpr int kWordsPerBlock = 1024;  // u32 words per (tile, group)
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Row n of a tile <-> storage position p.
+__host__ __device__ inline int tile_pos_of_row(int r) { return 16 * (r & 3) + (r >> 2); }
+__host__ __device__ inline int tile_row_of_pos(int p) { return 4 * (p & 15) + (p >> 4); }
+// Element e of a word <-> nibble slot.
+__host__ __device__ inline int slot_of_elem(int e) { return (e & 1) * 4 + (e >> 1); }
+
+// One packed word -> 8 bf16 values 128 + q, elements 0..7 in order.
+__device__ __forceinline__ u32x4 nib8_bits(uint32_t w) {
+  u32x4 r;
+  r[0] = (w & 0x000F000Fu) | 0x43004300u;
+  r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+  r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+  r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 nib8(uint32_t w) {
+  return __builtin_bit_cast(bf16x8, nib8_bits(w));
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 for a pair (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ uint16_t to_bf16(float f) {
+  return (uint16_t)(pack_bf16x2(f, 0.f) & 0xffffu);
+}
+
+}  // namespace qw4
+
+// Host-side helpers shared by the C-ABI translation units.
+namespace qw4 {
+void set_hip_error(int e);
+}
+#define QW4_LAUNCH_CHECK()                                   \
+  do {                                                       \
+    hipError_t e_ = hipGetLastError();                       \
+    if (e_ != hipSuccess) {                                  \
+      qw4::set_hip_error((int)e_);                           \
+      return QW4_ERR_HIP;                                    \
+    }                                                        \
+  } while (0)

@@ -1,0 +1,274 @@
+"""Python host binding of libqwen_w4a16.so (the C-ABI in include/qwen_w4a16.h).
+
+The function names mirror the reference's C++ entry points (namespace qwen in
+src/kernels/gemv_w4a16.cuh, gemm_w4a16.cuh and elementwise.cuh) so callers and
+tests read like the reference's own gates. Device memory and streams come from
+torch tensors (plumbing only); every compute call goes through the HIP library,
+and there is no fallback: if the library is missing, loading fails loudly.
+
+Errors: the reference prints and aborts; here a non-zero status raises
+W4A16Error carrying the status code and message.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqwen_w4a16.so")
+
+QW4_OK = 0
+QW4_ERR_NULL = 1
+QW4_ERR_SHAPE = 2
+QW4_ERR_GROUP = 3
+QW4_ERR_M = 4
+QW4_ERR_SCRATCH = 5
+QW4_ERR_ALIGN = 6
+QW4_ERR_HIP = 7
+QW4_ERR_NOMEM = 8
+QW4_ERR_LAYOUT = 9
+LAYOUT_AWQ_K = 1
+LAYOUT_AWQ_N = 2
+
+# Every symbol include/qwen_w4a16.h declares.
+EXPORTS = (
+    "qw4_status_string", "qw4_last_hip_error", "qw4_version", "qw4_weights_bytes",
+    "qw4_weights_alloc", "qw4_weights_free", "qw4_repack_ct_into", "qw4_repack_ct",
+    "qw4_repack_awq_into", "qw4_dequant_rows", "qw4_scratch_alloc", "qw4_scratch_free",
+    "qw4_partial_check", "qw4_choose_splits", "qw4_gemv", "qw4_gemv_f32", "qw4_gemm_small",
+    "qw4_gemm_mma", "qw4_gemv_argmax", "qw4_workspace_alloc", "qw4_workspace_free",
+    "qw4_gemm", "qw4_argmax", "qw4_argmax_rows", "qw4_gen_bf16", "qw4_gen_awq_k",
+)
+
+
+class W4A16Error(RuntimeError):
+    def __init__(self, status: int, where: str):
+        self.status = status
+        msg = lib().qw4_status_string(status).decode()
+        if status == QW4_ERR_HIP:
+            msg += f" (hipError {lib().qw4_last_hip_error()})"
+        super().__init__(f"{where}: {msg} [status {status}]")
+
+
+class W4A16Weights(C.Structure):
+    """qw4_weights / the reference's W4A16Weights (gemv_w4a16.cuh:50-60)."""
+    _fields_ = [("qweight", C.c_void_p), ("scale", C.c_void_p), ("zeros", C.c_void_p),
+                ("out_f", C.c_int32), ("in_f", C.c_int32), ("group_size", C.c_int32),
+                ("num_groups", C.c_int32)]
+
+    def total_bytes(self) -> int:
+        return lib().qw4_weights_bytes(C.byref(self))
+
+
+class GemvScratch(C.Structure):
+    """qw4_scratch / the reference's GemvScratch (gemv_w4a16.cuh:94-104)."""
+    _fields_ = [("partial", C.c_void_p), ("counters", C.c_void_p), ("keys", C.c_void_p),
+                ("partial_elems", C.c_size_t), ("max_in", C.c_int32), ("max_out", C.c_int32),
+                ("max_m", C.c_int32), ("max_tiles", C.c_int32)]
+
+
+class GemmWorkspace(C.Structure):
+    """qw4_workspace / the reference's GemmWorkspace (gemm_w4a16.cuh:30-35)."""
+    _fields_ = [("buf", C.c_void_p), ("bytes", C.c_size_t)]
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} not built: run __graft_entry__.build() "
+                          "(python qwen38-3090-cuda-server_amd/build.py)")
+    L = C.CDLL(LIB_PATH)
+    vp, i, sz, u64 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64
+    W, S, WS = C.POINTER(W4A16Weights), C.POINTER(GemvScratch), C.POINTER(GemmWorkspace)
+    sig = {
+        "qw4_status_string": ([i], C.c_char_p),
+        "qw4_last_hip_error": ([], i),
+        "qw4_version": ([], i),
+        "qw4_weights_bytes": ([W], sz),
+        "qw4_weights_alloc": ([W, i, i, i, vp], i),
+        "qw4_weights_free": ([W], i),
+        "qw4_repack_ct_into": ([W, i, vp, vp, vp, i, vp], i),
+        "qw4_repack_ct": ([W, vp, vp, vp, i, i, i, vp], i),
+        "qw4_repack_awq_into": ([W, i, vp, vp, vp, i, i, vp], i),
+        "qw4_dequant_rows": ([vp, W, i, i, vp], i),
+        "qw4_scratch_alloc": ([S, i, i, i, i], i),
+        "qw4_scratch_free": ([S], i),
+        "qw4_partial_check": ([S, i, i, i], i),
+        "qw4_choose_splits": ([i, i], i),
+        "qw4_gemv": ([vp, W, vp, S, vp], i),
+        "qw4_gemv_f32": ([vp, W, vp, S, vp], i),
+        "qw4_gemm_small": ([vp, W, vp, i, S, vp], i),
+        "qw4_gemm_mma": ([vp, W, vp, i, S, vp], i),
+        "qw4_gemv_argmax": ([vp, W, vp, i, S, vp], i),
+        "qw4_workspace_alloc": ([WS, sz], i),
+        "qw4_workspace_free": ([WS], i),
+        "qw4_gemm": ([vp, W, vp, i, WS, vp], i),
+        "qw4_argmax": ([vp, vp, i, vp, vp], i),
+        "qw4_argmax_rows": ([vp, vp, i, i, vp], i),
+        "qw4_gen_bf16": ([vp, sz, u64, u64, u64, i, vp], i),
+        "qw4_gen_awq_k": ([vp, vp, vp, i, i, u64, u64, vp], i),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(L, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = L
+    return L
+
+
+def _chk(status: int, where: str) -> None:
+    if status != QW4_OK:
+        raise W4A16Error(status, where)
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr() if hasattr(t, "data_ptr") else int(t)
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+
+        return torch.cuda.current_stream().cuda_stream
+    return stream.cuda_stream if hasattr(stream, "cuda_stream") else int(stream)
+
+
+# ------------------------------------------------------------- weights
+def awq_alloc_fused(total_out_f: int, in_f: int, group_size: int = 128, stream=None) -> W4A16Weights:
+    """awq_alloc_fused (gemv_w4a16.cuh:81-82)."""
+    w = W4A16Weights()
+    _chk(lib().qw4_weights_alloc(C.byref(w), total_out_f, in_f, group_size, _stream(stream)),
+         "awq_alloc_fused")
+    return w
+
+
+def awq_repack_into(w: W4A16Weights, row_offset: int, packed, scale, zp, out_f: int,
+                    stream=None) -> None:
+    """awq_repack_into (gemv_w4a16.cuh:83-85): compressed-tensors source tensors."""
+    _chk(lib().qw4_repack_ct_into(C.byref(w), row_offset, _ptr(packed), _ptr(scale), _ptr(zp),
+                                  out_f, _stream(stream)), "awq_repack_into")
+
+
+def awq_repack(packed, scale, zp, out_f: int, in_f: int, group_size: int = 128,
+               stream=None) -> W4A16Weights:
+    """awq_repack (gemv_w4a16.cuh:70-75)."""
+    w = W4A16Weights()
+    _chk(lib().qw4_repack_ct(C.byref(w), _ptr(packed), _ptr(scale), _ptr(zp), out_f, in_f,
+                             group_size, _stream(stream)), "awq_repack")
+    return w
+
+
+def awq_repack_awq_into(w: W4A16Weights, row_offset: int, qweight, scales, zeros, out_f: int,
+                        layout: int = LAYOUT_AWQ_K, stream=None) -> None:
+    """AWQ-order sources (BASELINE layout along K, or AutoAWQ along N)."""
+    _chk(lib().qw4_repack_awq_into(C.byref(w), row_offset, _ptr(qweight), _ptr(scales),
+                                   _ptr(zeros), out_f, layout, _stream(stream)),
+         "awq_repack_awq_into")
+
+
+def awq_free(w: W4A16Weights) -> None:
+    """awq_free (gemv_w4a16.cuh:86)."""
+    _chk(lib().qw4_weights_free(C.byref(w)), "awq_free")
+
+
+def w4a16_dequant_rows(dst, w: W4A16Weights, row0: int, nrows: int, stream=None) -> None:
+    """w4a16_dequant_rows (gemm_w4a16.cuh:45-48)."""
+    _chk(lib().qw4_dequant_rows(_ptr(dst), C.byref(w), row0, nrows, _stream(stream)),
+         "w4a16_dequant_rows")
+
+
+# ------------------------------------------------------------- scratch
+def gemv_scratch_alloc(max_in: int, max_out: int, min_group: int = 128, max_m: int = 1) -> GemvScratch:
+    """gemv_scratch_alloc (gemv_w4a16.cuh:106-107)."""
+    s = GemvScratch()
+    _chk(lib().qw4_scratch_alloc(C.byref(s), max_in, max_out, min_group, max_m),
+         "gemv_scratch_alloc")
+    return s
+
+
+def gemv_scratch_free(s: GemvScratch) -> None:
+    _chk(lib().qw4_scratch_free(C.byref(s)), "gemv_scratch_free")
+
+
+def gemv_partial_check(s: GemvScratch, splits: int, out_f: int, M: int) -> None:
+    _chk(lib().qw4_partial_check(C.byref(s), splits, out_f, M), "gemv_partial_check")
+
+
+def gemv_choose_splits(out_f: int, num_groups: int) -> int:
+    return lib().qw4_choose_splits(out_f, num_groups)
+
+
+def gemm_workspace_alloc(nbytes: int = 0) -> GemmWorkspace:
+    ws = GemmWorkspace()
+    _chk(lib().qw4_workspace_alloc(C.byref(ws), nbytes), "gemm_workspace_alloc")
+    return ws
+
+
+def gemm_workspace_free(ws: GemmWorkspace) -> None:
+    _chk(lib().qw4_workspace_free(C.byref(ws)), "gemm_workspace_free")
+
+
+# ------------------------------------------------------------- compute
+def gemv_w4a16(y, w: W4A16Weights, x, s: GemvScratch, stream=None) -> None:
+    """gemv_w4a16 (gemv_w4a16.cuh:130-131): y[out] = W @ x, bf16."""
+    _chk(lib().qw4_gemv(_ptr(y), C.byref(w), _ptr(x), C.byref(s), _stream(stream)), "gemv_w4a16")
+
+
+def gemv_w4a16_f32(y, w: W4A16Weights, x, s: GemvScratch, stream=None) -> None:
+    """gemv_w4a16_f32 (gemv_w4a16.cuh:132-133)."""
+    _chk(lib().qw4_gemv_f32(_ptr(y), C.byref(w), _ptr(x), C.byref(s), _stream(stream)),
+         "gemv_w4a16_f32")
+
+
+def gemm_small_w4a16(y, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """gemm_small_w4a16 (gemv_w4a16.cuh:124-125): Y[M,out] = X[M,in] @ W^T."""
+    _chk(lib().qw4_gemm_small(_ptr(y), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
+         "gemm_small_w4a16")
+
+
+def gemm_mma_w4a16(y, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """gemm_mma_w4a16 (gemv_w4a16.cuh:187-188)."""
+    _chk(lib().qw4_gemm_mma(_ptr(y), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
+         "gemm_mma_w4a16")
+
+
+def gemv_argmax_w4a16(idx, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """lm_head GEMV + fused fp32 row-argmax (model.cu:796-815 + elementwise.cuh:39-43)."""
+    _chk(lib().qw4_gemv_argmax(_ptr(idx), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
+         "gemv_argmax_w4a16")
+
+
+def gemm_w4a16(Cm, w: W4A16Weights, A, M: int, ws: GemmWorkspace | None = None, stream=None) -> None:
+    """gemm_w4a16 (gemm_w4a16.cuh:40-43): C[M,out] = A[M,in] @ W^T."""
+    wsp = C.byref(ws) if ws is not None else None
+    _chk(lib().qw4_gemm(_ptr(Cm), C.byref(w), _ptr(A), M, wsp, _stream(stream)), "gemm_w4a16")
+
+
+def argmax(out, x, n: int, scratch, stream=None) -> None:
+    """argmax (elementwise.cuh:39-40) over bf16 logits."""
+    _chk(lib().qw4_argmax(_ptr(out), _ptr(x), n, _ptr(scratch), _stream(stream)), "argmax")
+
+
+def argmax_rows(out, x, rows: int, n: int, stream=None) -> None:
+    """argmax_rows (elementwise.cuh:41-43)."""
+    _chk(lib().qw4_argmax_rows(_ptr(out), _ptr(x), rows, n, _stream(stream)), "argmax_rows")
+
+
+# ------------------------------------------------------ synthetic inputs
+def gen_bf16(out, count: int, seed: int, stream_id: int, kind: int, offset: int = 0,
+             stream=None) -> None:
+    _chk(lib().qw4_gen_bf16(_ptr(out), count, seed, stream_id, offset, kind, _stream(stream)),
+         "gen_bf16")
+
+
+def gen_awq_k(qweight, scales, zeros, out_f: int, in_f: int, seed: int, tensor: int,
+              stream=None) -> None:
+    _chk(lib().qw4_gen_awq_k(_ptr(qweight), _ptr(scales), _ptr(zeros), out_f, in_f, seed,
+                             tensor, _stream(stream)), "gen_awq_k")

@@ -1,0 +1,103 @@
+"""The C-ABI library loads, exports every symbol include/qwen_w4a16.h declares,
+and rejects bad arguments with status codes before touching the GPU (CPU only:
+no call here launches work)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qwen_w4a16.h")
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import w4a16_hip
+
+    w4a16_hip.lib()
+    return w4a16_hip
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(qw4_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree(hip):
+    assert declared_functions() == sorted(hip.EXPORTS)
+
+
+def test_every_declared_symbol_exported(hip):
+    L = C.CDLL(hip.LIB_PATH)
+    for name in declared_functions():
+        assert hasattr(L, name), name
+
+
+def test_status_strings(hip):
+    L = hip.lib()
+    for code in range(10):
+        assert L.qw4_status_string(code)
+    assert L.qw4_status_string(0) == b"ok"
+
+
+def _fake_weights(hip, out_f=128, in_f=512, group=128):
+    w = hip.W4A16Weights()
+    w.qweight, w.scale, w.zeros = 0x1000, 0x2000, 0x3000   # never dereferenced
+    w.out_f, w.in_f, w.group_size, w.num_groups = out_f, in_f, group, in_f // group
+    return w
+
+
+def _fake_scratch(hip, max_m=16, tiles=4):
+    s = hip.GemvScratch()
+    s.partial, s.counters, s.keys = 0x4000, 0x5000, 0x6000
+    s.partial_elems, s.max_in, s.max_out, s.max_m, s.max_tiles = 1 << 20, 512, 256, max_m, tiles
+    return s
+
+
+def test_argument_errors_before_any_launch(hip):
+    L = hip.lib()
+    w, s = _fake_weights(hip), _fake_scratch(hip)
+    x, y = C.c_void_p(0x10000), C.c_void_p(0x20000)
+    # M out of range (reference: gemv_w4a16.cu:429 aborts on M outside 2..16)
+    assert L.qw4_gemm_small(y, C.byref(w), x, 17, C.byref(s), None) == hip.QW4_ERR_M
+    assert L.qw4_gemm_small(y, C.byref(w), x, 0, C.byref(s), None) == hip.QW4_ERR_M
+    assert L.qw4_gemv_argmax(y, C.byref(w), x, 17, C.byref(s), None) == hip.QW4_ERR_M
+    # group other than 128 (reference: gemv_w4a16.cu:392 aborts)
+    wg = _fake_weights(hip, group=64)
+    assert L.qw4_gemv(y, C.byref(wg), x, C.byref(s), None) == hip.QW4_ERR_GROUP
+    # shapes the layout cannot hold
+    assert L.qw4_gemv(y, C.byref(_fake_weights(hip, out_f=96)), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    assert L.qw4_gemv(y, C.byref(_fake_weights(hip, in_f=640)), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    # scratch too small for the output rows / M (reference: gemv_partial_check aborts)
+    small = _fake_scratch(hip, max_m=4, tiles=1)
+    assert L.qw4_gemv(y, C.byref(w), x, C.byref(small), None) == hip.QW4_ERR_SCRATCH
+    assert L.qw4_gemm_small(y, C.byref(w), x, 9, C.byref(_fake_scratch(hip, max_m=4)), None) == hip.QW4_ERR_SCRATCH
+    # misaligned activations
+    assert L.qw4_gemv(y, C.byref(w), C.c_void_p(0x10002), C.byref(s), None) == hip.QW4_ERR_ALIGN
+    # null pointers
+    assert L.qw4_gemv(None, C.byref(w), x, C.byref(s), None) == hip.QW4_ERR_NULL
+    assert L.qw4_gemm(y, C.byref(w), x, 0, None, None) == hip.QW4_ERR_M
+    assert L.qw4_repack_ct_into(C.byref(w), 32, x, x, x, 64, None) == hip.QW4_ERR_SHAPE   # offset % 64
+    assert L.qw4_repack_ct_into(C.byref(w), 64, x, x, x, 128, None) == hip.QW4_ERR_SHAPE  # overflow
+    assert L.qw4_repack_awq_into(C.byref(w), 0, x, x, x, 128, 7, None) == hip.QW4_ERR_LAYOUT
+    assert L.qw4_dequant_rows(y, C.byref(w), 100, 64, None) == hip.QW4_ERR_SHAPE
+    assert L.qw4_argmax_rows(y, x, 1, 0, None) == hip.QW4_ERR_SHAPE
+    assert L.qw4_partial_check(C.byref(small), 4, 128, 1) == hip.QW4_ERR_SCRATCH
+
+
+def test_python_binding_raises(hip):
+    w, s = _fake_weights(hip), _fake_scratch(hip)
+    with pytest.raises(hip.W4A16Error) as e:
+        hip.gemm_small_w4a16(0x20000, w, 0x10000, 17, s, stream=0)
+    assert e.value.status == hip.QW4_ERR_M
+
+
+def test_choose_splits_fills_the_chip(hip):
+    # small-N shapes split K, wide ones do not; splits never exceed G/4
+    assert hip.gemv_choose_splits(248320, 40) == 1
+    for n, g in ((5120, 40), (7168, 40), (5120, 32), (5120, 136), (34816, 40)):
+        s = hip.gemv_choose_splits(n, g)
+        assert 1 <= s <= g // 4
+        assert (n // 64) * s >= min(1024, (n // 64) * (g // 4))
