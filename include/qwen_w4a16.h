@@ -172,6 +172,11 @@ int qw4_gen_bf16(uint16_t* out, size_t count, uint64_t seed, uint64_t stream_id,
 int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_f,
                   int in_f, uint64_t seed, uint64_t tensor, void* stream);
 
+/* Streaming-read microbenchmark (no reference counterpart; the intent of the
+ * reference's bench/microbench.cu "streaming read"): reads `bytes` (multiple of
+ * 16) with 16-byte loads and writes one XOR per workgroup to sink[blocks]. */
+int qw4_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,7 +82,7 @@ __device__ __forceinline__ uint32_t deq_pair(uint32_t magic, float s, float c) {
 }
 
 __device__ __forceinline__ void store_stage(const Stage& st, uint16_t* sA, uint16_t* sB,
-                                            int tid) {
+                                            int tid, NibConst kc) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int id = tid + 256 * i;
@@ -100,7 +100,7 @@ __device__ __forceinline__ void store_stage(const Stage& st, uint16_t* sA, uint1
     uint16_t* dst = sB + row * LDA + 32 * j;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const u32x4 m = nib8_bits(st.w[i][w]);
+      const u32x4 m = nib8_bits(st.w[i][w], kc);
       *reinterpret_cast<u32x4*>(dst + 8 * w) =
           u32x4{deq_pair(m[0], s, c), deq_pair(m[1], s, c), deq_pair(m[2], s, c),
                 deq_pair(m[3], s, c)};
@@ -123,10 +123,11 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  const NibConst kc = nib_const();
   Stage st;
   load_stage(st, a, m0, n0, 0, tid);
   for (int g = 0; g < a.G; ++g) {
-    store_stage(st, sA, sB, tid);
+    store_stage(st, sA, sB, tid, kc);
     __syncthreads();
     if (g + 1 < a.G) load_stage(st, a, m0, n0, g + 1, tid);
 #pragma unroll

@@ -193,6 +193,28 @@ __global__ void k_gen_awq_k_meta(uint16_t* sc, uint32_t* zr, int N, int G, uint6
   }
 }
 
+// Streaming read: grid-stride 16-byte loads, XOR-folded so nothing is dead code.
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ src, size_t n16,
+                                                     uint32_t* sink) {
+  u32x4 acc = {0, 0, 0, 0};
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i);
+    const u32x4 b = __builtin_nontemporal_load(src + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+  uint32_t v = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
+  for (int off = 32; off > 0; off >>= 1) v ^= __shfl_xor(v, off, 64);
+  __shared__ uint32_t part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = part[0] ^ part[1] ^ part[2] ^ part[3];
+}
+
 int check_weights(const qw4_weights* w) {
   if (!w || !w->qweight || !w->scale || !w->zeros) return QW4_ERR_NULL;
   if (w->group_size != kGroup) return QW4_ERR_GROUP;
@@ -357,6 +379,16 @@ int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_
   const size_t nm = (size_t)(in_f / kGroup) * (out_f / 8);
   k_gen_awq_k_meta<<<(unsigned)std::min<size_t>(blocks_for(nm, 256), 65536), 256, 0, hs>>>(
       scales, zeros, out_f, in_f / kGroup, seed, tensor);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  if (!src || !sink) return QW4_ERR_NULL;
+  if (bytes % 16 || blocks <= 0) return QW4_ERR_SHAPE;
+  if ((uintptr_t)src & 15) return QW4_ERR_ALIGN;
+  k_stream_read<<<blocks, 256, 0, (hipStream_t)stream>>>(static_cast<const u32x4*>(src),
+                                                         bytes / 16, sink);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
 }

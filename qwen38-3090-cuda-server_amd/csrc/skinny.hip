@@ -20,6 +20,13 @@
 //     (per-tile counter) sums them in split order 0..S-1, so results are
 //     bitwise deterministic (the property of gemv_w4a16.cu:262-279), and resets
 //     the counter so the next call -- or a graph replay -- starts from zero.
+//   * Cross-workgroup exchange never flushes or invalidates an L2: each XCD has
+//     its own L2, and a device-scope fence (buffer_wbl2 + buffer_inv) per
+//     workgroup costs more than the whole weight stream. Only the exchanged
+//     words are made coherent: partials are written through to memory
+//     (system-scope relaxed stores, sc0 sc1), the writer waits for their
+//     completion (s_waitcnt) before its memory-side counter increment (sc1), and
+//     the last workgroup reads them back with memory-coherent loads.
 //
 // Output layout per lane after the loop: acc[st][jj] is row m = 4q + jj,
 // column n = 64*tile + 4c + st.
@@ -47,10 +54,17 @@ struct SkinnyArgs {
   const uint16_t* x;
   void* y;
   float* partial;
-  uint32_t* counters;   // [tiles] arrival counters, then [tiles] the argmax counter
-  uint64_t* keys;       // [16] argmax keys
-  int M, N, K, G, S, tiles;
+  uint32_t* counters;   // one counter per 128-byte line (kCounterStride words):
+                        //   [0, tiles)            split arrival, per tile
+                        //   [max_tiles, +64)      argmax arrival, per key group
+                        //   [max_tiles + 64]      argmax arrival, of key groups
+  uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
+  int M, N, K, G, S, tiles, max_tiles;
 };
+
+// Memory-side atomics on one cache line serialize; each counter gets its own line.
+constexpr int kCounterStride = 32;
+constexpr int kKeyGroups = 64;
 
 // Monotonic key: larger value first, then lower index (elementwise.cu:103-104).
 __device__ __forceinline__ uint64_t argmax_key(float v, int n) {
@@ -58,6 +72,19 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int n) {
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
   return ((uint64_t)u << 32) | (uint64_t)(~(uint32_t)n);
 }
+
+// Coherent scalar exchange between workgroups of one launch (see header).
+__device__ __forceinline__ void st_sys(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_sys(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t inc_sys(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this wave issued has completed.
+__device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 struct GroupData {
   u32x4 w[4];   // row quad st -> 4 words (k chunks t = 0..3)
@@ -80,7 +107,7 @@ __device__ __forceinline__ void load_group(GroupData& d, const SkinnyArgs& a, in
   d.z = a.zr[blk * 16 + c];
 }
 
-__device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d) {
+__device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, NibConst k) {
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
                                                        0x3F803F80u, 0x3F803F80u});
   f32x4 C[4], Cs;
@@ -89,7 +116,7 @@ __device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d) {
     const bf16x8 A = __builtin_bit_cast(bf16x8, d.x[t]);
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      const bf16x8 B = nib8(d.w[st][t]);
+      const bf16x8 B = nib8(d.w[st][t], k);
       C[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
           A, B, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : C[st], 0, 0, 0);
     }
@@ -123,13 +150,19 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyArgs a) {
   for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (g0 < g1) {
-    GroupData cur, nxt;
-    load_group(cur, a, b, g0, c, q, xrow);
-    for (int g = g0; g < g1; ++g) {
-      if (g + 1 < g1) load_group(nxt, a, b, g + 1, c, q, xrow);
-      mma_group(acc, cur);
-      cur = nxt;
+    const NibConst k = nib_const();
+    // Ping-pong buffers: the loads of group g+1 are in flight during the MFMAs
+    // of group g, with no register copies between iterations.
+    GroupData d0, d1;
+    load_group(d0, a, b, g0, c, q, xrow);
+    int g = g0;
+    for (; g + 1 < g1; g += 2) {
+      load_group(d1, a, b, g + 1, c, q, xrow);
+      mma_group(acc, d0, k);
+      if (g + 2 < g1) load_group(d0, a, b, g + 2, c, q, xrow);
+      mma_group(acc, d1, k);
     }
+    if (g < g1) mma_group(acc, d0, k);
   }
 
   // Sum the four waves in wave order.
@@ -146,28 +179,32 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyArgs a) {
   }
 
   if (a.S > 1) {
-    float* mine = a.partial + ((size_t)b * a.S + s) * 1024 + lane * 16;
+    // Partial layout: [tile][split][lane][16], element 4*st + jj.
     if (wave == 0) {
+      float* mine = a.partial + ((size_t)b * a.S + s) * 1024 + lane * 16;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) reinterpret_cast<f32x4*>(mine)[st] = acc[st];
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) st_sys(mine + 4 * st + jj, acc[st][jj]);
+      wait_all_mem();
     }
-    __threadfence();
     __syncthreads();
-    if (threadIdx.x == 0) s_last = (atomicAdd(&a.counters[b], 1u) == (unsigned)(a.S - 1));
+    if (threadIdx.x == 0) s_last = inc_sys(&a.counters[b * kCounterStride]) == (uint32_t)(a.S - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    if (wave == 0) {
-      const float* base = a.partial + (size_t)b * a.S * 1024 + lane * 16;
+    if (wave != 0) return;
+    const float* base = a.partial + (size_t)b * a.S * 1024 + lane * 16;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
-      for (int sp = 0; sp < a.S; ++sp) {
+    for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int sp = 0; sp < a.S; ++sp) {
 #pragma unroll
-        for (int st = 0; st < 4; ++st)
-          acc[st] += __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(base + (size_t)sp * 1024) + st);
-      }
-      if (lane == 0) a.counters[b] = 0;
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[st][jj] += ld_sys(base + (size_t)sp * 1024 + 4 * st + jj);
     }
+    if (lane == 0)
+      __hip_atomic_store(&a.counters[b * kCounterStride], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
   if (wave != 0) return;
 
@@ -191,6 +228,12 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyArgs a) {
             f32x4{acc[0][jj], acc[1][jj], acc[2][jj], acc[3][jj]};
     }
   } else {
+    // Two-level argmax without hot spots: tile b folds its best (value, index)
+    // per row into key group b % 64 (one cache line per group); the last tile
+    // of a group to arrive bumps the group counter, and the last group to
+    // finish folds the 64 groups, writes the indices and clears the state.
+    const int grp = b % kKeyGroups;
+    uint64_t* gkeys = a.keys + grp * 16;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       float v = acc[0][jj];
@@ -205,20 +248,35 @@ __global__ __launch_bounds__(256) void k_skinny(SkinnyArgs a) {
         if (v2 > v || (v2 == v && n2 < n)) { v = v2; n = n2; }
       }
       const int m = 4 * q + jj;
-      if (c == 0 && m < a.M) atomicMax((unsigned long long*)&a.keys[m], (unsigned long long)argmax_key(v, n));
+      if (c == 0 && m < a.M)
+        __hip_atomic_fetch_max(&gkeys[m], argmax_key(v, n), __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
     }
-    __threadfence();
+    wait_all_mem();   // this tile's key updates are complete before it is counted
     if (lane == 0) {
-      uint32_t* done = a.counters + a.tiles;
-      if (atomicAdd(done, 1u) == (unsigned)(a.tiles - 1)) {
-        __threadfence();
+      const int ngroups = a.tiles < kKeyGroups ? a.tiles : kKeyGroups;
+      const uint32_t in_grp = (uint32_t)((a.tiles - 1 - grp) / kKeyGroups + 1);
+      uint32_t* gcnt = a.counters + (size_t)(a.max_tiles + grp) * kCounterStride;
+      uint32_t* done = a.counters + (size_t)(a.max_tiles + kKeyGroups) * kCounterStride;
+      if (inc_sys(gcnt) == in_grp - 1 && inc_sys(done) == (uint32_t)(ngroups - 1)) {
         int32_t* idx = static_cast<int32_t*>(a.y);
         for (int m = 0; m < a.M; ++m) {
-          const uint64_t k = __hip_atomic_load(&a.keys[m], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          idx[m] = (int32_t)(~(uint32_t)(k & 0xffffffffu));
-          a.keys[m] = 0;
+          uint64_t best = 0;
+          for (int g2 = 0; g2 < ngroups; ++g2) {
+            const uint64_t k = __hip_atomic_load(&a.keys[g2 * 16 + m], __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            best = k > best ? k : best;
+          }
+          idx[m] = (int32_t)(~(uint32_t)(best & 0xffffffffu));
         }
-        *done = 0;
+        for (int g2 = 0; g2 < ngroups; ++g2) {
+          for (int m = 0; m < a.M; ++m)
+            __hip_atomic_store(&a.keys[g2 * 16 + m], (uint64_t)0, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.counters + (size_t)(a.max_tiles + g2) * kCounterStride, 0u,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -278,6 +336,7 @@ int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scra
   a.G = w->num_groups;
   a.S = S;
   a.tiles = tiles;
+  a.max_tiles = s->max_tiles;
   k_skinny<OUT><<<tiles * S, 256, 0, (hipStream_t)stream>>>(a);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
@@ -307,12 +366,13 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
   s->max_tiles = (max_out + kTileN - 1) / kTileN;
   // Any out_f <= max_out: S > 1 implies tiles * S < 2 * target.
   s->partial_elems = (size_t)2 * target_wgs() * 1024;
-  const size_t cnt_bytes = (size_t)(s->max_tiles + 1) * 4;
+  const size_t cnt_bytes = (size_t)(s->max_tiles + kKeyGroups + 1) * kCounterStride * 4;
+  const size_t key_bytes = (size_t)kKeyGroups * 16 * 8;
   hipError_t e = hipMalloc((void**)&s->partial, s->partial_elems * 4);
   if (e == hipSuccess) e = hipMalloc((void**)&s->counters, cnt_bytes);
-  if (e == hipSuccess) e = hipMalloc((void**)&s->keys, 16 * 8);
+  if (e == hipSuccess) e = hipMalloc((void**)&s->keys, key_bytes);
   if (e == hipSuccess) e = hipMemset(s->counters, 0, cnt_bytes);
-  if (e == hipSuccess) e = hipMemset(s->keys, 0, 16 * 8);
+  if (e == hipSuccess) e = hipMemset(s->keys, 0, key_bytes);
   if (e == hipSuccess) e = hipDeviceSynchronize();
   if (e != hipSuccess) {
     set_hip_error((int)e);

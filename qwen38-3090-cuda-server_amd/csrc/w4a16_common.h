@@ -44,18 +44,34 @@ __host__ __device__ inline int tile_row_of_pos(int p) { return 4 * (p & 15) + (p
 // Element e of a word <-> nibble slot.
 __host__ __device__ inline int slot_of_elem(int e) { return (e & 1) * 4 + (e >> 1); }
 
+// Nibble-unpack constants held in VGPRs. gfx9-family VOP3 encodings take at
+// most one scalar/literal operand, so with both constants as literals the
+// compiler emits v_and + v_or per pair; with the constants in opaque VGPRs
+// (materialized once, hoisted out of loops) it selects one v_and_or_b32.
+// Only the materialization is asm; the arithmetic stays visible to the
+// compiler, which inserts the VALU -> MFMA wait states itself.
+struct NibConst {
+  uint32_t mask, magic;
+};
+__device__ __forceinline__ NibConst nib_const() {
+  NibConst c;
+  asm volatile("v_mov_b32 %0, 0x000f000f" : "=v"(c.mask));
+  asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(c.magic));
+  return c;
+}
+
 // One packed word -> 8 bf16 values 128 + q, elements 0..7 in order.
-__device__ __forceinline__ u32x4 nib8_bits(uint32_t w) {
+__device__ __forceinline__ u32x4 nib8_bits(uint32_t w, NibConst k) {
   u32x4 r;
-  r[0] = (w & 0x000F000Fu) | 0x43004300u;
-  r[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-  r[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-  r[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+  r[0] = (w & k.mask) | k.magic;
+  r[1] = ((w >> 4) & k.mask) | k.magic;
+  r[2] = ((w >> 8) & k.mask) | k.magic;
+  r[3] = ((w >> 12) & k.mask) | k.magic;
   return r;
 }
 
-__device__ __forceinline__ bf16x8 nib8(uint32_t w) {
-  return __builtin_bit_cast(bf16x8, nib8_bits(w));
+__device__ __forceinline__ bf16x8 nib8(uint32_t w, NibConst k) {
+  return __builtin_bit_cast(bf16x8, nib8_bits(w, k));
 }
 
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t h) {

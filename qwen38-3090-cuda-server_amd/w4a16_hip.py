@@ -38,6 +38,7 @@ EXPORTS = (
     "qw4_partial_check", "qw4_choose_splits", "qw4_gemv", "qw4_gemv_f32", "qw4_gemm_small",
     "qw4_gemm_mma", "qw4_gemv_argmax", "qw4_workspace_alloc", "qw4_workspace_free",
     "qw4_gemm", "qw4_argmax", "qw4_argmax_rows", "qw4_gen_bf16", "qw4_gen_awq_k",
+    "qw4_stream_read",
 )
 
 
@@ -112,6 +113,7 @@ def lib():
         "qw4_argmax_rows": ([vp, vp, i, i, vp], i),
         "qw4_gen_bf16": ([vp, sz, u64, u64, u64, i, vp], i),
         "qw4_gen_awq_k": ([vp, vp, vp, i, i, u64, u64, vp], i),
+        "qw4_stream_read": ([vp, sz, vp, i, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -130,6 +132,15 @@ def _ptr(t) -> int | None:
     if t is None:
         return None
     return t.data_ptr() if hasattr(t, "data_ptr") else int(t)
+
+
+def _need(t, nbytes: int, where: str) -> None:
+    """Host-side bounds check before a launch: a torch tensor argument must hold
+    at least nbytes (raw integer pointers cannot be checked and are trusted)."""
+    if t is not None and hasattr(t, "numel") and hasattr(t, "element_size"):
+        have = t.numel() * t.element_size()
+        if have < nbytes:
+            raise ValueError(f"{where}: buffer holds {have} bytes, needs {nbytes}")
 
 
 def _stream(stream) -> int | None:
@@ -152,6 +163,10 @@ def awq_alloc_fused(total_out_f: int, in_f: int, group_size: int = 128, stream=N
 def awq_repack_into(w: W4A16Weights, row_offset: int, packed, scale, zp, out_f: int,
                     stream=None) -> None:
     """awq_repack_into (gemv_w4a16.cuh:83-85): compressed-tensors source tensors."""
+    G = w.in_f // 128
+    _need(packed, out_f * w.in_f // 2, "awq_repack_into packed")
+    _need(scale, out_f * G * 2, "awq_repack_into scale")
+    _need(zp, out_f // 8 * G * 4, "awq_repack_into zp")
     _chk(lib().qw4_repack_ct_into(C.byref(w), row_offset, _ptr(packed), _ptr(scale), _ptr(zp),
                                   out_f, _stream(stream)), "awq_repack_into")
 
@@ -159,6 +174,10 @@ def awq_repack_into(w: W4A16Weights, row_offset: int, packed, scale, zp, out_f: 
 def awq_repack(packed, scale, zp, out_f: int, in_f: int, group_size: int = 128,
                stream=None) -> W4A16Weights:
     """awq_repack (gemv_w4a16.cuh:70-75)."""
+    G = in_f // group_size if group_size else 0
+    _need(packed, out_f * in_f // 2, "awq_repack packed")
+    _need(scale, out_f * G * 2, "awq_repack scale")
+    _need(zp, out_f // 8 * G * 4, "awq_repack zp")
     w = W4A16Weights()
     _chk(lib().qw4_repack_ct(C.byref(w), _ptr(packed), _ptr(scale), _ptr(zp), out_f, in_f,
                              group_size, _stream(stream)), "awq_repack")
@@ -168,6 +187,10 @@ def awq_repack(packed, scale, zp, out_f: int, in_f: int, group_size: int = 128,
 def awq_repack_awq_into(w: W4A16Weights, row_offset: int, qweight, scales, zeros, out_f: int,
                         layout: int = LAYOUT_AWQ_K, stream=None) -> None:
     """AWQ-order sources (BASELINE layout along K, or AutoAWQ along N)."""
+    G = w.in_f // 128
+    _need(qweight, out_f * w.in_f // 2, "awq_repack_awq_into qweight")
+    _need(scales, out_f * G * 2, "awq_repack_awq_into scales")
+    _need(zeros, out_f // 8 * G * 4, "awq_repack_awq_into zeros")
     _chk(lib().qw4_repack_awq_into(C.byref(w), row_offset, _ptr(qweight), _ptr(scales),
                                    _ptr(zeros), out_f, layout, _stream(stream)),
          "awq_repack_awq_into")
@@ -180,6 +203,7 @@ def awq_free(w: W4A16Weights) -> None:
 
 def w4a16_dequant_rows(dst, w: W4A16Weights, row0: int, nrows: int, stream=None) -> None:
     """w4a16_dequant_rows (gemm_w4a16.cuh:45-48)."""
+    _need(dst, max(nrows, 0) * w.in_f * 2, "w4a16_dequant_rows dst")
     _chk(lib().qw4_dequant_rows(_ptr(dst), C.byref(w), row0, nrows, _stream(stream)),
          "w4a16_dequant_rows")
 
@@ -218,57 +242,87 @@ def gemm_workspace_free(ws: GemmWorkspace) -> None:
 # ------------------------------------------------------------- compute
 def gemv_w4a16(y, w: W4A16Weights, x, s: GemvScratch, stream=None) -> None:
     """gemv_w4a16 (gemv_w4a16.cuh:130-131): y[out] = W @ x, bf16."""
+    _need(y, w.out_f * 2, "gemv_w4a16 y")
+    _need(x, w.in_f * 2, "gemv_w4a16 x")
     _chk(lib().qw4_gemv(_ptr(y), C.byref(w), _ptr(x), C.byref(s), _stream(stream)), "gemv_w4a16")
 
 
 def gemv_w4a16_f32(y, w: W4A16Weights, x, s: GemvScratch, stream=None) -> None:
     """gemv_w4a16_f32 (gemv_w4a16.cuh:132-133)."""
+    _need(y, w.out_f * 4, "gemv_w4a16_f32 y")
+    _need(x, w.in_f * 2, "gemv_w4a16_f32 x")
     _chk(lib().qw4_gemv_f32(_ptr(y), C.byref(w), _ptr(x), C.byref(s), _stream(stream)),
          "gemv_w4a16_f32")
 
 
 def gemm_small_w4a16(y, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
     """gemm_small_w4a16 (gemv_w4a16.cuh:124-125): Y[M,out] = X[M,in] @ W^T."""
+    _need(y, max(M, 0) * w.out_f * 2, "gemm_small_w4a16 y")
+    _need(x, max(M, 0) * w.in_f * 2, "gemm_small_w4a16 x")
     _chk(lib().qw4_gemm_small(_ptr(y), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
          "gemm_small_w4a16")
 
 
 def gemm_mma_w4a16(y, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
     """gemm_mma_w4a16 (gemv_w4a16.cuh:187-188)."""
+    _need(y, max(M, 0) * w.out_f * 2, "gemm_mma_w4a16 y")
+    _need(x, max(M, 0) * w.in_f * 2, "gemm_mma_w4a16 x")
     _chk(lib().qw4_gemm_mma(_ptr(y), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
          "gemm_mma_w4a16")
 
 
 def gemv_argmax_w4a16(idx, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
     """lm_head GEMV + fused fp32 row-argmax (model.cu:796-815 + elementwise.cuh:39-43)."""
+    _need(idx, max(M, 0) * 4, "gemv_argmax_w4a16 idx")
+    _need(x, max(M, 0) * w.in_f * 2, "gemv_argmax_w4a16 x")
     _chk(lib().qw4_gemv_argmax(_ptr(idx), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
          "gemv_argmax_w4a16")
 
 
 def gemm_w4a16(Cm, w: W4A16Weights, A, M: int, ws: GemmWorkspace | None = None, stream=None) -> None:
     """gemm_w4a16 (gemm_w4a16.cuh:40-43): C[M,out] = A[M,in] @ W^T."""
+    _need(Cm, max(M, 0) * w.out_f * 2, "gemm_w4a16 C")
+    _need(A, max(M, 0) * w.in_f * 2, "gemm_w4a16 A")
     wsp = C.byref(ws) if ws is not None else None
     _chk(lib().qw4_gemm(_ptr(Cm), C.byref(w), _ptr(A), M, wsp, _stream(stream)), "gemm_w4a16")
 
 
 def argmax(out, x, n: int, scratch, stream=None) -> None:
     """argmax (elementwise.cuh:39-40) over bf16 logits."""
+    _need(out, 4, "argmax out")
+    _need(x, n * 2, "argmax x")
+    _need(scratch, 512 * 4, "argmax scratch")
     _chk(lib().qw4_argmax(_ptr(out), _ptr(x), n, _ptr(scratch), _stream(stream)), "argmax")
 
 
 def argmax_rows(out, x, rows: int, n: int, stream=None) -> None:
     """argmax_rows (elementwise.cuh:41-43)."""
+    _need(out, rows * 4, "argmax_rows out")
+    _need(x, rows * n * 2, "argmax_rows x")
     _chk(lib().qw4_argmax_rows(_ptr(out), _ptr(x), rows, n, _stream(stream)), "argmax_rows")
 
 
 # ------------------------------------------------------ synthetic inputs
 def gen_bf16(out, count: int, seed: int, stream_id: int, kind: int, offset: int = 0,
              stream=None) -> None:
+    _need(out, count * 2, "gen_bf16 out")
     _chk(lib().qw4_gen_bf16(_ptr(out), count, seed, stream_id, offset, kind, _stream(stream)),
          "gen_bf16")
 
 
 def gen_awq_k(qweight, scales, zeros, out_f: int, in_f: int, seed: int, tensor: int,
               stream=None) -> None:
+    G = in_f // 128
+    _need(qweight, in_f // 8 * out_f * 4, "gen_awq_k qweight")
+    _need(scales, G * out_f * 2, "gen_awq_k scales")
+    _need(zeros, G * out_f // 8 * 4, "gen_awq_k zeros")
     _chk(lib().qw4_gen_awq_k(_ptr(qweight), _ptr(scales), _ptr(zeros), out_f, in_f, seed,
                              tensor, _stream(stream)), "gen_awq_k")
+
+
+def stream_read(src, nbytes: int, sink, blocks: int, stream=None) -> None:
+    """Streaming-read microbenchmark kernel (HBM read bandwidth denominator)."""
+    _need(src, nbytes, "stream_read src")
+    _need(sink, blocks * 4, "stream_read sink")
+    _chk(lib().qw4_stream_read(_ptr(src), nbytes, _ptr(sink), blocks, _stream(stream)),
+         "stream_read")
