@@ -109,8 +109,9 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
 int qw4_scratch_free(qw4_scratch* s);
 /* gemv_partial_check (gemv_w4a16.cuh:109-110; .cu:359-366), as a status code. */
 int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
-/* gemv_choose_splits (gemv_w4a16.cuh:134; .cu:289-306): K-splits the skinny
- * kernel uses for this shape (env QW4_SKINNY_WGS overrides the target). */
+/* gemv_choose_splits (gemv_w4a16.cuh:134; .cu:289-306): cross-workgroup
+ * K-splits the skinny kernel uses for this shape (1 unless out_f is too small
+ * to occupy the chip; env QW4_SKINNY_W / QW4_SKINNY_S override, for tuning). */
 int qw4_choose_splits(int out_f, int num_groups);
 
 /* ------------------------------------------------------- decode / verify
