@@ -157,35 +157,72 @@ def main():
         for lw in layers:
             for (name, K, N), w in zip(LAYER, lw):
                 if per_launch is not None:
-                    e0 = T.event()
+                    e0 = torch.cuda.Event(enable_timing=True, external=True)
+                    e0.record()
                 if M == 1:
                     hip.gemv_w4a16(ys, w, xs[K], scratch)
                 else:
                     hip.gemm_small_w4a16(ys, w, xs[K], M, scratch)
                 if per_launch is not None:
-                    per_launch.append((name, e0, T.event()))
+                    e1 = torch.cuda.Event(enable_timing=True, external=True)
+                    e1.record()
+                    per_launch.append((name, e0, e1))
+
+    def capture(fn):
+        """One decode step as a hipGraph (the reference replays its decode step
+        as a CUDA graph, src/model/model.cu:880-946): no host launch gaps."""
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        g.replay()
+        torch.cuda.synchronize()
+        return g
+
+    def time_graph(g, iters):
+        a = T.event()
+        for _ in range(iters):
+            g.replay()
+        b = T.event()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
 
     # ------------------------------------------------- headline: config 2
+    g_step = capture(step)
     for _ in range(args.warmup):
-        step()
+        g_step.replay()
     torch.cuda.synchronize()
     e0 = T.event()
     for _ in range(args.steps):
-        step()
+        g_step.replay()
     e1 = T.event()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
     value = step_bytes / (ms * 1e-3) / 1e9
     log(f"config2: {ms:.3f} ms/step, {value:.1f} GB/s")
 
-    # per-launch durations of the same sweep (the roofline's kernel time)
-    rec = []
-    for _ in range(max(2, args.steps // 4)):
-        step(per_launch=rec)
-    torch.cuda.synchronize()
+    # per-launch kernel durations of the same sweep: timing events captured
+    # around every launch inside a second graph
     per = {}
-    for name, a, b in rec:
-        per.setdefault(name, []).append(a.elapsed_time(b))
+    try:
+        rec = []
+        g_prof = capture(lambda: step(per_launch=rec))
+        rec_last = rec[-len(LAYER) * args.layers:]
+        for _ in range(3):
+            g_prof.replay()
+            torch.cuda.synchronize()
+            for name, a, b in rec_last:
+                per.setdefault(name, []).append(a.elapsed_time(b))
+        extra["kernel_timing"] = "HIP events captured around each launch in a graph"
+    except Exception as exc:  # event nodes unsupported: per-shape graphs
+        log(f"per-launch events in graph unavailable ({exc}); timing per-shape graphs")
+        per = {}
+        for li, (name, K, N) in enumerate(LAYER):
+            g1 = capture(lambda: [hip.gemv_w4a16(ys, lw[li], xs[K], scratch) for lw in layers])
+            t = time_graph(g1, 3)
+            per[name] = [t / len(layers)] * len(layers)
+        extra["kernel_timing"] = "per-shape graphs of 64 launches (includes inter-kernel gaps)"
     tot_ms, tot_bytes, launches = 0.0, 0, 0
     per_op = {}
     for name, K, N in LAYER:
@@ -221,33 +258,22 @@ def main():
     if not args.only_decode:
         # ---------------------------------------------------------- config 1
         w1 = make_weights(hip, torch, 5120, 5120, 0, 9001, tmp)
-        for _ in range(10):
-            hip.gemv_w4a16(ys, w1, xs[5120], scratch)
-        a = T.event()
-        for _ in range(200):
-            hip.gemv_w4a16(ys, w1, xs[5120], scratch)
-        b = T.event()
-        torch.cuda.synchronize()
-        us = a.elapsed_time(b) / 200 * 1e3
+        g1 = capture(lambda: [hip.gemv_w4a16(ys, w1, xs[5120], scratch) for _ in range(100)])
+        us = time_graph(g1, 5) / 100 * 1e3
         extra["config1"] = {"us_per_call": round(us, 2),
                             "GBps": round(alg_bytes(1, 5120, 5120) / (us * 1e-6) / 1e9, 1),
-                            "note": "13.6 MB back to back: MALL-resident, launch-bound"}
+                            "note": "13.6 MB, 100 calls in one graph: MALL-resident"}
         hip.awq_free(w1)
 
         # ---------------------------------------------------------- config 3
         c3 = {}
         for M in (9, 12, 16):
-            step(M)
-            torch.cuda.synchronize()
-            a = T.event()
-            for _ in range(5):
-                step(M)
-            b = T.event()
-            torch.cuda.synchronize()
-            msM = a.elapsed_time(b) / 5
+            gM = capture(lambda: step(M))
+            msM = time_graph(gM, 5)
             byM = sum(alg_bytes(M, K, N) for _, K, N in LAYER) * args.layers
             c3[f"M{M}"] = {"ms_per_sweep": round(msM, 3), "GBps": round(byM / (msM * 1e-3) / 1e9, 1),
                            "x_of_M1": round(msM / ms, 3)}
+            del gM
         extra["config3_verify"] = c3
         log(f"config3: {c3}")
 
@@ -256,16 +282,12 @@ def main():
         idx = torch.empty(16, dtype=torch.int32, device="cuda")
         c5 = {}
         for M in (1, 9):
-            for _ in range(3):
-                hip.gemv_argmax_w4a16(idx, wl, xs[5120], M, scratch)
-            a = T.event()
-            for _ in range(20):
-                hip.gemv_argmax_w4a16(idx, wl, xs[5120], M, scratch)
-            b = T.event()
-            torch.cuda.synchronize()
-            us = a.elapsed_time(b) / 20 * 1e3
+            g5 = capture(lambda: [hip.gemv_argmax_w4a16(idx, wl, xs[5120], M, scratch)
+                                  for _ in range(10)])
+            us = time_graph(g5, 3) / 10 * 1e3
             bts = alg_bytes(M, 5120, 248320, out=False)
             c5[f"M{M}"] = {"us_per_call": round(us, 2), "GBps": round(bts / (us * 1e-6) / 1e9, 1)}
+            del g5
         extra["config5_lm_head_argmax"] = c5
         hip.awq_free(wl)
         log(f"config5: {c5}")

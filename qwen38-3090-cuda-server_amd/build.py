@@ -27,7 +27,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
     "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
     f"-I{os.path.join(ROOT, 'include')}",
-]
+] + os.environ.get("QW4_EXTRA_CFLAGS", "").split()
 # Packed FP32 (v_pk_*_f32) is disabled on the device side; hipcc's host pass warns
 # that it does not know the feature, which is harmless.
 DEVICE = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",

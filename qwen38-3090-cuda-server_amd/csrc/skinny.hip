@@ -9,33 +9,40 @@
 // U = tiles x groups blocks (one 4 KiB (tile, group) block each) is cut into P
 // equal contiguous ranges. A workgroup walks the tiles its range touches; a
 // tile it covers completely it finishes itself, a tile cut by a range boundary
-// is finished by whichever of its (at most a few) workgroups arrives last.
+// ("split tile") is finished by whichever contributor completes it last.
 //
 // Per block, a wave streams 4 KiB with four 16-byte loads per lane (lane
 // c + 16q reads chunk q of positions 16*st + c, i.e. rows 4c + st) and feeds
 // bf16 MFMA v_mfma_f32_16x16x32_bf16:
-//    A = activations, 16 rows (rows >= M are zero), 32 k per instruction
+//    A = activations, 16 rows (rows >= M read a zero row), 32 k per instruction
 //    B = the packed word turned into 8 bf16 values (128 + q) by AND-OR
 // Four instructions per row quad st cover the group; a fifth B operand of ones
 // gives S_m = sum_k x[m][k] in the same output layout, so the zero-point and
 // +128 correction is
 //    acc[m][n] += s[n] * (C[m][n] - (128 + zp[n]) * S_m)
 // (the reference's identity, src/kernels/gemv_w4a16.cuh:25-37, with the group
-// sum computed by the matrix core instead of a prologue kernel). The 4 waves of
-// a workgroup take interleaved blocks of each tile and are summed through LDS.
+// sum computed by the matrix core instead of a prologue kernel). The W waves of
+// a workgroup take interleaved blocks of each tile (two loads in flight, then
+// two blocks of math; latency is hidden by occupancy) and are summed in LDS.
 //
-// Determinism: a tile's sum is always formed in the same order (waves 0..3 in
-// LDS; partial workgroups in workgroup order), so repeated calls are bitwise
-// identical (the property of gemv_w4a16.cu:262-279).
-//
-// Cross-workgroup exchange never flushes or invalidates an L2 (each XCD has its
-// own, and a device-scope fence per workgroup costs more than the weight
-// stream). Only the exchanged data is made coherent: partials are written
-// through with 16-byte device-coherent (sc1) buffer stores, the writer waits
-// for completion (s_waitcnt) before its device-scope counter increment, and the
-// last workgroup reads them back with sc1 loads. Counters sit one per 128-byte
-// line and reset themselves, so the next call -- or a graph replay -- starts
-// from zero.
+// Split tiles, without fences or L2 flushes (each XCD has its own L2; a
+// device-scope fence per workgroup costs more than the weight stream):
+//  * M = 1: each contributor adds its partial, as 2^-20 fixed point biased by
+//    2^49, into one 64-bit word per output element with a returning
+//    device-scope atomic, together with 1 << 56 as an arrival count. Integer
+//    addition is order-independent (bitwise deterministic), and the contributor
+//    whose add completes the count holds the exact total in the returned value,
+//    rounds it once and emits it, then clears the word. One round trip; a
+//    workgroup's first split tile is stashed in LDS and issued together with its
+//    last at the end, so no wave stalls mid-stream. Limits: |partial| < 2^29
+//    and at most 64 contributors per tile (ranges are kept >= G/60 blocks).
+//  * M > 1: each contributor writes its partial through (16-byte sc1 buffer
+//    stores) to its slot, waits for completion once at the end of the
+//    workgroup, then bumps the tile's counter (one per 128-byte line); the last
+//    one reads all slots back (sc1 loads) in workgroup order and emits.
+// Counters and words reset themselves, so the next call -- or a graph replay --
+// starts from zero. Whole tiles are summed in a fixed order (waves 0..W-1), so
+// every output is bitwise reproducible (the property of gemv_w4a16.cu:262-279).
 //
 // Output layout per lane: acc[st][jj] is row m = 4q + jj, column
 // n = 64*tile + 4c + st.
@@ -62,21 +69,28 @@ constexpr int kKeyGroups = 64;
 // The most workgroups per CU a scratch buffer is sized for.
 constexpr int kMaxWgsPerCu = 8;
 
+// Fixed-point split-tile accumulation (M = 1).
+constexpr float kFixScale = 1048576.0f;   // 2^20 (exact scaling)
+constexpr long long kFixBias = 1LL << 49;
+constexpr uint64_t kFixCount = 1ull << 56;
+constexpr uint64_t kFixMask = kFixCount - 1;
+
 struct SkinnyArgs {
   const uint32_t* qw;
   const uint16_t* sc;
   const uint16_t* zr;
   const uint16_t* x;
   void* y;
-  float* partial;       // [P][2 slots][4 st][64 lanes] f32x4
+  float* slots;         // M > 1: [P][2][4 st][64 lanes] f32x4 partials
+  uint64_t* sums;       // M = 1: [tiles][64 columns] accumulators
   uint32_t* counters;   // one counter per 128-byte line (kCounterStride words):
-                        //   [0, tiles)            partial-tile arrival, per tile
+                        //   [0, max_tiles)        split-tile arrival (M > 1)
                         //   [max_tiles, +64)      argmax arrival, per key group
                         //   [max_tiles + 64]      argmax arrival, of key groups
   uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
   const uint16_t* zero_row;   // >= K bf16 zeros: the activation row of lanes m >= M
   int M, N, K, G, tiles, max_tiles, P, U;
-  uint32_t partial_bytes;
+  uint32_t slot_bytes;
 };
 
 // Monotonic key: larger value first, then lower index (elementwise.cu:103-104).
@@ -95,15 +109,15 @@ __device__ __forceinline__ void clear_dev(uint32_t* p) {
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
-// 16-byte device-coherent (sc1) accesses to the partial buffer.
+// 16-byte device-coherent (sc1) accesses to the slot buffer (M > 1).
 constexpr int kCpolSc1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t partial_rsrc(const SkinnyArgs& a) {
-  return __builtin_amdgcn_make_buffer_rsrc(a.partial, 0, (int)a.partial_bytes, 0x00020000);
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const SkinnyArgs& a) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)a.slot_bytes, 0x00020000);
 }
-__device__ __forceinline__ void st_partial(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+__device__ __forceinline__ void st_slot(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCpolSc1);
 }
-__device__ __forceinline__ f32x4 ld_partial(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+__device__ __forceinline__ f32x4 ld_slot(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
 }
 
@@ -165,8 +179,9 @@ __device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, N
   }
 }
 
+// ------------------------------------------------------------- epilogues
 // Running argmax of one workgroup: per lane, the best (value, column) of rows
-// m = 4q + jj over the tiles this workgroup finished.
+// m = 4q + jj over the elements this workgroup finished.
 struct Best {
   float v[4];
   int n[4];
@@ -177,6 +192,13 @@ __device__ __forceinline__ void best_init(Best& bs) {
   for (int jj = 0; jj < 4; ++jj) {
     bs.v[jj] = -__builtin_inff();
     bs.n[jj] = 0x7fffffff;
+  }
+}
+
+__device__ __forceinline__ void best_fold(Best& bs, int jj, float v, int n) {
+  if (v > bs.v[jj] || (v == bs.v[jj] && n < bs.n[jj])) {
+    bs.v[jj] = v;
+    bs.n[jj] = n;
   }
 }
 
@@ -209,15 +231,97 @@ __device__ __forceinline__ void emit_tile(const SkinnyArgs& a, int b, const f32x
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const float v = acc[st][jj];
-        const int n = n0 + st;
-        if (v > bs.v[jj] || (v == bs.v[jj] && n < bs.n[jj])) {
-          bs.v[jj] = v;
-          bs.n[jj] = n;
-        }
-      }
+      for (int st = 0; st < 4; ++st) best_fold(bs, jj, acc[st][jj], n0 + st);
   }
+}
+
+// M = 1: add this workgroup's partials of split tiles b0 (if h0) and b1 (if h1)
+// -- rows m = 0, held by lanes q = 0 in acc[st][0] -- and emit every element
+// this workgroup completes. All atomics are issued before any result is used.
+template <int OUT>
+__device__ __forceinline__ void fix_add_emit(const SkinnyArgs& a, int lane, Best& bs, int b0,
+                                             const f32x4 (&acc0)[4], bool h0, int b1,
+                                             const f32x4 (&acc1)[4], bool h1) {
+  const int c = lane & 15, q = lane >> 4;
+  if (q != 0) return;
+  uint64_t tot[2][4], add[2][4];
+  uint64_t* w[2][4];
+  const int bb[2] = {b0, b1};
+  const bool hh[2] = {h0, h1};
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (!hh[i]) continue;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      long long f = __float2ll_rn((i ? acc1[st][0] : acc0[st][0]) * kFixScale);
+      f = f > kFixBias - 1 ? kFixBias - 1 : (f < 1 - kFixBias ? 1 - kFixBias : f);
+      add[i][st] = kFixCount + (uint64_t)(f + kFixBias);
+      w[i][st] = a.sums + (size_t)bb[i] * 64 + 4 * c + st;
+      tot[i][st] = __hip_atomic_fetch_add(w[i][st], add[i][st], __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (!hh[i]) continue;
+    const uint64_t S =
+        (uint64_t)(owner_of(a, bb[i] * a.G + a.G - 1) - owner_of(a, bb[i] * a.G) + 1);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const uint64_t t = tot[i][st] + add[i][st];
+      if ((t >> 56) == S) {
+        const long long v = (long long)(t & kFixMask) - (long long)S * kFixBias;
+        __hip_atomic_store(w[i][st], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // one rounding: int64 -> fp32, then an exact power-of-two scale
+        const float val = (float)v * (1.0f / kFixScale);
+        const int n = bb[i] * kTileN + 4 * c + st;
+        if (OUT == OUT_BF16)
+          static_cast<uint16_t*>(a.y)[n] = to_bf16(val);
+        else if (OUT == OUT_F32)
+          static_cast<float*>(a.y)[n] = val;
+        else
+          best_fold(bs, 0, val, n);
+      }
+    }
+  }
+}
+
+// M > 1: write this workgroup's partial of split tile b through to its slot
+// (0: the tile is its first, 1: its last).
+__device__ __forceinline__ void slot_store(const SkinnyArgs& a, int p, bool first_tile,
+                                           const f32x4 (&acc)[4], int lane) {
+  const int q = lane >> 4;
+  if (4 * q >= a.M) return;   // lanes holding only rows m >= M
+  const __amdgpu_buffer_rsrc_t r = slot_rsrc(a);
+  const uint32_t off = (uint32_t)((p * 2 + (first_tile ? 0 : 1)) * 4096 + lane * 16);
+#pragma unroll
+  for (int st = 0; st < 4; ++st) st_slot(r, off + st * 1024, acc[st]);
+}
+
+// M > 1, after this workgroup's slots are complete: count it in for tile b;
+// the last contributor sums the slots in workgroup order p0..p1 and emits.
+template <int OUT>
+__device__ __forceinline__ void slot_arrive(const SkinnyArgs& a, int b, int lane, Best& bs) {
+  const int p0 = owner_of(a, b * a.G), p1 = owner_of(a, b * a.G + a.G - 1);
+  uint32_t old = 0;
+  if (lane == 0) old = inc_dev(&a.counters[b * kCounterStride]);
+  old = __shfl(old, 0, 64);
+  if (old != (uint32_t)(p1 - p0)) return;
+  const int q = lane >> 4;
+  const __amdgpu_buffer_rsrc_t r = slot_rsrc(a);
+  f32x4 acc[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (4 * q < a.M) {
+    for (int pp = p0; pp <= p1; ++pp) {
+      const int slot = (pp == p0 && range_start(a, pp) / a.G != b) ? 1 : 0;
+      const uint32_t off = (uint32_t)((pp * 2 + slot) * 4096 + lane * 16);
+#pragma unroll
+      for (int st = 0; st < 4; ++st) acc[st] += ld_slot(r, off + st * 1024);
+    }
+  }
+  if (lane == 0) clear_dev(&a.counters[b * kCounterStride]);
+  emit_tile<OUT>(a, b, acc, lane, bs);
 }
 
 // Wave 0 at the end of an argmax workgroup: fold the workgroup's best per row
@@ -271,65 +375,18 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
   }
 }
 
-// Wave 0: the summed segment [lo, hi) of tile b is complete for this
-// workgroup. A whole tile is emitted at once; a partial one is only written
-// through to this workgroup's slot (0: its first tile, 1: its last) -- the
-// completion wait and the arrival count happen once, in arrive_partial, after
-// the workgroup's last segment, so no wave stalls on them mid-stream.
-template <int OUT>
-__device__ __forceinline__ bool store_segment(const SkinnyArgs& a, int p, int b, int lo, int hi,
-                                              bool first_tile, const f32x4 (&acc)[4], int lane,
-                                              Best& bs) {
-  if (lo == 0 && hi == a.G) {
-    emit_tile<OUT>(a, b, acc, lane, bs);
-    return false;
-  }
-  const int q = lane >> 4;
-  if (4 * q < a.M) {   // lanes holding rows m < M
-    const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a);
-    const uint32_t mine = (uint32_t)((p * 2 + (first_tile ? 0 : 1)) * 4096 + lane * 16);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) st_partial(pr, mine + st * 1024, acc[st]);
-  }
-  return true;
-}
-
-// Wave 0, after all partial slots of this workgroup are written and complete:
-// count this workgroup in for tile b; the last contributor sums the partials in
-// workgroup order p0..p1 and emits the tile.
-template <int OUT>
-__device__ __forceinline__ void arrive_partial(const SkinnyArgs& a, int b, int lane, Best& bs) {
-  const int p0 = owner_of(a, b * a.G), p1 = owner_of(a, b * a.G + a.G - 1);
-  uint32_t old = 0;
-  if (lane == 0) old = inc_dev(&a.counters[b * kCounterStride]);
-  old = __shfl(old, 0, 64);
-  if (old != (uint32_t)(p1 - p0)) return;
-  const int q = lane >> 4;
-  const __amdgpu_buffer_rsrc_t pr = partial_rsrc(a);
-  f32x4 acc[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (4 * q < a.M) {
-    for (int pp = p0; pp <= p1; ++pp) {
-      const int slot = (pp == p0 && range_start(a, pp) / a.G != b) ? 1 : 0;
-      const uint32_t off = (uint32_t)((pp * 2 + slot) * 4096 + lane * 16);
-#pragma unroll
-      for (int st = 0; st < 4; ++st) acc[st] += ld_partial(pr, off + st * 1024);
-    }
-  }
-  if (lane == 0) clear_dev(&a.counters[b * kCounterStride]);
-  emit_tile<OUT>(a, b, acc, lane, bs);
-}
-
-// W waves per workgroup. Inside a tile segment each wave takes groups
-// lo + wave, lo + wave + W, ... in batches of two blocks: both loads issued,
-// then both computed. Latency is hidden by occupancy (about 128 VGPRs, 4 waves
-// per SIMD) rather than by a deep per-wave ring. W = 4: LDS sums double-buffered
-// per segment; W = 8: one buffer and a second barrier.
-template <int OUT, int W>
+// ----------------------------------------------------------------- kernel
+// W waves per workgroup; M1: the fixed-point exchange (M = 1) or the slot
+// exchange (M > 1). Inside a tile segment each wave takes groups lo + wave,
+// lo + wave + W, ... in batches of two blocks (one for W = 16, to fit 128
+// VGPRs). W = 4: LDS sums double-buffered per segment; W >= 8: one buffer and
+// a second barrier.
+template <int OUT, int W, bool M1>
 __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   constexpr int kNbuf = W == 4 ? 2 : 1;
+  constexpr int kBatch = W == 16 ? 1 : 2;
   __shared__ f32x4 red[kNbuf][W - 1][4][64];
+  __shared__ f32x4 stash[4][64];   // M = 1: the first split tile's sums
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
   const uint16_t* xrow = (c < a.M ? a.x + (size_t)c * a.K : a.zero_row) + 32 * q;
@@ -342,7 +399,8 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   const NibConst k = nib_const();
 
   int par = 0;
-  bool part_first = false, part_last = false;   // partial slots written (wave 0)
+  bool split_first = false, split_last = false;   // wave 0
+  f32x4 last_acc[4];
   Best bs;
   best_init(bs);
   for (int sb = bfirst; sb <= blast; ++sb) {
@@ -351,9 +409,9 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
     f32x4 acc[4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int g = lo + wave; g < hi; g += 2 * W) {
+    for (int g = lo + wave; g < hi; g += kBatch * W) {
       GroupData d0, d1;
-      const bool two = g + W < hi;
+      const bool two = kBatch == 2 && g + W < hi;
       load_group(d0, a, sb, g, c, q, xrow);
       if (two) load_group(d1, a, sb, g + W, c, q, xrow);
       mma_group(acc, d0, k);
@@ -369,35 +427,57 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
       for (int w = 0; w < W - 1; ++w)
 #pragma unroll
         for (int st = 0; st < 4; ++st) acc[st] += red[par][w][st][lane];
-      const bool part = store_segment<OUT>(a, p, sb, lo, hi, sb == bfirst, acc, lane, bs);
-      if (sb == bfirst) part_first = part;
-      else part_last = part;
+      if (lo == 0 && hi == a.G) {
+        emit_tile<OUT>(a, sb, acc, lane, bs);
+      } else if (sb == bfirst) {
+        split_first = true;
+        if (M1) {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) stash[st][lane] = acc[st];
+        } else {
+          slot_store(a, p, true, acc, lane);
+        }
+      } else {
+        split_last = true;
+        if (M1) {
+#pragma unroll
+          for (int st = 0; st < 4; ++st) last_acc[st] = acc[st];
+        } else {
+          slot_store(a, p, false, acc, lane);
+        }
+      }
     }
     if (kNbuf == 2)
       par ^= 1;
     else
       __syncthreads();   // red is reused by the next segment
   }
-  if (wave == 0 && (part_first || part_last)) {
-    wait_all_mem();   // partial slots complete before they are counted
-    if (part_first) arrive_partial<OUT>(a, bfirst, lane, bs);
-    if (part_last) arrive_partial<OUT>(a, blast, lane, bs);
+  if (wave == 0 && (split_first || split_last)) {
+    if (M1) {
+      f32x4 first_acc[4];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) first_acc[st] = stash[st][lane];
+      fix_add_emit<OUT>(a, lane, bs, bfirst, first_acc, split_first, blast, last_acc,
+                        split_last);
+    } else {
+      wait_all_mem();   // slots complete before they are counted
+      if (split_first) slot_arrive<OUT>(a, bfirst, lane, bs);
+      if (split_last) slot_arrive<OUT>(a, blast, lane, bs);
+    }
   }
   if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
 }
 
 // ------------------------------------------------------------- host side
 // Workgroups per CU: the kernel's occupancy (all workgroups resident in one
-// round, equal work each), or QW4_SKINNY_WGS_PER_CU (tuning only).
-int g_env_wgs = 0;
+// round, equal work each). QW4_SKINNY_WGS_PER_CU, QW4_SKINNY_W (4|8|16) and
+// QW4_SKINNY_WG_TILES (tiles x 4 / n workgroups) override it, for tuning only.
+int g_env_wgs = 0, g_env_tiles_per_wg = 0, g_env_w = 0;
 std::once_flag g_env_once;
 int g_cus[64] = {0};
-int g_occ[64][3][2] = {{{0}}};
-int g_env_w = 0;   // QW4_SKINNY_W=4|8 (tuning)
+int g_occ[64][3][3][2] = {{{{0}}}};
 
-int g_env_tiles_per_wg = 0;   // QW4_SKINNY_WG_TILES=n: n/4 tiles per workgroup (tuning)
-
-int env_wgs_per_cu() {
+void read_env() {
   std::call_once(g_env_once, [] {
     const char* e = std::getenv("QW4_SKINNY_WGS_PER_CU");
     const int v = e ? std::atoi(e) : 0;
@@ -407,7 +487,6 @@ int env_wgs_per_cu() {
     const char* w = std::getenv("QW4_SKINNY_W");
     g_env_w = w ? std::atoi(w) : 0;
   });
-  return g_env_wgs;
 }
 
 int current_device() {
@@ -428,14 +507,14 @@ int device_cus() {
   return g_cus[dev];
 }
 
-template <int OUT, int W>
+template <int OUT, int W, bool M1>
 int wgs_per_cu() {
-  if (env_wgs_per_cu()) return env_wgs_per_cu();
-  const int dev = current_device();
-  int& slot = g_occ[dev][OUT][W == 4 ? 0 : 1];
+  read_env();
+  if (g_env_wgs) return g_env_wgs;
+  int& slot = g_occ[current_device()][OUT][W == 4 ? 0 : (W == 8 ? 1 : 2)][M1 ? 1 : 0];
   if (!slot) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_skinny<OUT, W>, 64 * W, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_skinny<OUT, W, M1>, 64 * W, 0) !=
             hipSuccess ||
         n <= 0)
       n = 1;
@@ -448,45 +527,70 @@ struct Launch {
   int W, P;
 };
 
-// W = 8 with one workgroup per tile when the tiles alone cannot give every CU
-// a workgroup and K is short enough for few blocks per wave; otherwise W = 4
-// stream-K over every resident slot.
-template <int OUT>
+// Default: W = 4 stream-K over every resident slot. Small outputs with short K
+// (measured on MI355X: the 19 MB qkv and 11 MB o projections) do better with
+// more waves per tile and fewer split tiles: M = 1 uses W = 16 with two
+// workgroups per tile, M > 1 W = 8 with one.
+template <int OUT, bool M1>
 Launch launch_for(int out_f, int G) {
-  env_wgs_per_cu();
+  read_env();
   const int tiles = out_f / kTileN;
   const long long U = (long long)tiles * G;
+  const bool small = tiles < device_cus() && G <= 48 && U <= 5000;
   Launch l;
-  l.W = (tiles < device_cus() && G <= 48) ? 8 : 4;
-  if (g_env_w == 4 || g_env_w == 8) l.W = g_env_w;
-  long long cap = (long long)device_cus() * (l.W == 4 ? wgs_per_cu<OUT, 4>() : wgs_per_cu<OUT, 8>());
-  if (l.W == 8) cap = tiles;
+  l.W = small ? (M1 ? 16 : 8) : 4;
+  if (g_env_w == 4 || g_env_w == 8 || g_env_w == 16) l.W = g_env_w;
+  long long cap;
+  if (l.W == 4)
+    cap = (long long)device_cus() * wgs_per_cu<OUT, 4, M1>();
+  else
+    cap = (long long)tiles * (l.W == 16 ? 2 : 1);
   if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
+  // at most 64 workgroups may share a tile: keep ranges >= G / 60 blocks
+  cap = std::min(cap, std::max<long long>(1, U * 60 / G));
   l.P = (int)std::max<long long>(1, std::min(cap, (U + l.W - 1) / l.W));
   return l;
 }
+
+template <int OUT, bool M1>
+void launch(const SkinnyArgs& a, int W, hipStream_t st) {
+  if (W == 16)
+    k_skinny<OUT, 16, M1><<<a.P, 1024, 0, st>>>(a);
+  else if (W == 8)
+    k_skinny<OUT, 8, M1><<<a.P, 512, 0, st>>>(a);
+  else
+    k_skinny<OUT, 4, M1><<<a.P, 256, 0, st>>>(a);
+}
+
+// Scratch regions inside qw4_scratch.partial: slots for the largest grid, then
+// the fixed-point words of every tile.
+size_t slot_floats() { return (size_t)device_cus() * kMaxWgsPerCu * 2 * 1024; }
 
 template <int OUT>
 int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scratch* s,
                void* stream) {
   int st = check_weights_public(w);
   if (st) return st;
-  if (!y || !x || !s || !s->counters || !s->partial) return QW4_ERR_NULL;
+  if (!y || !x || !s || !s->counters || !s->partial || !s->keys) return QW4_ERR_NULL;
   if (M < 1 || M > 16) return QW4_ERR_M;
   if (((uintptr_t)x & 15) || ((uintptr_t)y & (OUT == OUT_F32 ? 15 : (OUT == OUT_BF16 ? 7 : 3))))
     return QW4_ERR_ALIGN;
   const int tiles = w->out_f / kTileN;
-  if (tiles > s->max_tiles || M > s->max_m) return QW4_ERR_SCRATCH;
-  const Launch l = launch_for<OUT>(w->out_f, w->num_groups);
-  const int P = l.P;
-  if ((size_t)P * 2 * 1024 > s->partial_elems) return QW4_ERR_SCRATCH;
+  if (tiles > s->max_tiles || M > s->max_m || w->in_f > s->max_in) return QW4_ERR_SCRATCH;
+  const bool m1 = M == 1;
+  const Launch l = m1 ? launch_for<OUT, true>(w->out_f, w->num_groups)
+                      : launch_for<OUT, false>(w->out_f, w->num_groups);
+  if ((size_t)l.P * 2 * 1024 > slot_floats() ||
+      slot_floats() + (size_t)tiles * 64 * 2 > s->partial_elems)
+    return QW4_ERR_SCRATCH;
   SkinnyArgs a;
   a.qw = w->qweight;
   a.sc = w->scale;
   a.zr = w->zeros;
   a.x = x;
   a.y = y;
-  a.partial = s->partial;
+  a.slots = s->partial;
+  a.sums = reinterpret_cast<uint64_t*>(s->partial + slot_floats());
   a.counters = s->counters;
   a.keys = s->keys;
   a.zero_row = reinterpret_cast<const uint16_t*>(s->keys + kKeyGroups * 16);
@@ -496,13 +600,13 @@ int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scra
   a.G = w->num_groups;
   a.tiles = tiles;
   a.max_tiles = s->max_tiles;
-  a.P = P;
+  a.P = l.P;
   a.U = tiles * w->num_groups;
-  a.partial_bytes = (uint32_t)(s->partial_elems * 4);
-  if (l.W == 8)
-    k_skinny<OUT, 8><<<P, 512, 0, (hipStream_t)stream>>>(a);
+  a.slot_bytes = (uint32_t)(slot_floats() * 4);
+  if (m1)
+    launch<OUT, true>(a, l.W, (hipStream_t)stream);
   else
-    k_skinny<OUT, 4><<<P, 256, 0, (hipStream_t)stream>>>(a);
+    launch<OUT, false>(a, l.W, (hipStream_t)stream);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
 }
@@ -517,7 +621,7 @@ extern "C" {
 int qw4_choose_splits(int out_f, int num_groups) {
   if (out_f < kTileN || num_groups <= 0) return 1;
   const long long U = (long long)(out_f / kTileN) * num_groups;
-  const long long P = launch_for<OUT_BF16>(out_f, num_groups).P;
+  const long long P = launch_for<OUT_BF16, true>(out_f, num_groups).P;
   // workgroups sharing one tile, at most: ceil(G / blocks-per-workgroup) + 1
   const long long per = std::max<long long>(1, U / P);
   return (int)std::min<long long>(P, (num_groups + per - 1) / per + (U % P ? 1 : 0));
@@ -533,12 +637,13 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
   s->max_out = max_out;
   s->max_m = max_m;
   s->max_tiles = (max_out + kTileN - 1) / kTileN;
-  // two 4 KiB partial slots per stream-K workgroup, for the largest grid
-  s->partial_elems = (size_t)device_cus() * kMaxWgsPerCu * 2 * 1024;
+  // slots (M > 1) for the largest grid, then one fixed-point word per column
+  s->partial_elems = slot_floats() + (size_t)s->max_tiles * 64 * 2;
   const size_t cnt_bytes = (size_t)(s->max_tiles + kKeyGroups + 1) * kCounterStride * 4;
   // argmax keys, then a zero activation row of max_in bf16 (never written)
   const size_t key_bytes = (size_t)kKeyGroups * 16 * 8 + (size_t)max_in * 2 + 256;
   hipError_t e = hipMalloc((void**)&s->partial, s->partial_elems * 4);
+  if (e == hipSuccess) e = hipMemset(s->partial, 0, s->partial_elems * 4);
   if (e == hipSuccess) e = hipMalloc((void**)&s->counters, cnt_bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&s->keys, key_bytes);
   if (e == hipSuccess) e = hipMemset(s->counters, 0, cnt_bytes);
@@ -566,7 +671,7 @@ int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M) {
   if (!s) return QW4_ERR_NULL;
   (void)splits;
   if (M > s->max_m || (out_f + kTileN - 1) / kTileN > s->max_tiles) return QW4_ERR_SCRATCH;
-  const size_t need = (size_t)launch_for<OUT_BF16>(out_f, s->max_in / kGroup).P * 2 * 1024;
+  const size_t need = slot_floats() + (size_t)((out_f + kTileN - 1) / kTileN) * 64 * 2;
   return need > s->partial_elems ? QW4_ERR_SCRATCH : QW4_OK;
 }
 
