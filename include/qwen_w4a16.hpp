@@ -1,0 +1,102 @@
+// qwen_w4a16.hpp -- call-compatible C++ layer over the C-ABI (qwen_w4a16.h).
+//
+// The declarations keep the names, argument order and meaning of the
+// reference's namespace qwen entry points so its callers drop in with the type
+// substitutions __nv_bfloat16 -> __hip_bfloat16 (bit-identical) and
+// cudaStream_t -> hipStream_t:
+//   src/kernels/gemv_w4a16.cuh:50-135, :187-188   (W4A16 GEMV / skinny / MMA)
+//   src/kernels/gemm_w4a16.cuh:30-48              (prefill GEMM, dequant rows)
+//   src/kernels/elementwise.cuh:39-43              (argmax, argmax_rows)
+// Like the reference, these print a message and abort() on invalid input; the
+// C-ABI underneath returns status codes instead.
+//
+// Differences callers may observe (none changes a documented result):
+//   * W4A16Weights' device layout is private and differs (tile-major, 4-bit
+//     zero points); qweight / scale / zp are still three separate hipMalloc
+//     allocations, each freeable with hipFree.
+//   * GemvScratch holds split-K state instead of widened activations; its
+//     public fields max_m and partial_elems keep their meaning.
+//   * GemmWorkspace holds no BLAS handle: the prefill GEMM is one fused kernel.
+//   * group_size must be 128; out_f % 64 == 0 and in_f % 512 == 0.
+#pragma once
+#include <hip/hip_bf16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "qwen_w4a16.h"
+
+namespace qwen {
+
+struct W4A16Weights {
+  uint32_t* qweight = nullptr;
+  __hip_bfloat16* scale = nullptr;
+  uint8_t* zp = nullptr;   // 4-bit zero points, 4 rows per 16-bit word
+  int out_f = 0, in_f = 0, group_size = 0, num_groups = 0;
+
+  size_t qweight_bytes() const { return size_t(out_f) * in_f / 2; }
+  size_t scale_bytes() const { return size_t(out_f) * num_groups * 2; }
+  size_t zp_bytes() const { return size_t(out_f) * num_groups / 2; }
+  size_t total_bytes() const { return qweight_bytes() + scale_bytes() + zp_bytes(); }
+};
+
+// awq_repack (gemv_w4a16.cuh:70-75): compressed-tensors source tensors.
+void awq_repack(W4A16Weights& dst, const uint32_t* src_packed, const __hip_bfloat16* src_scale,
+                const uint32_t* src_zp, int out_f, int in_f, int group_size,
+                hipStream_t stream = 0);
+void awq_alloc_fused(W4A16Weights& dst, int total_out_f, int in_f, int group_size,
+                     hipStream_t stream = 0);
+void awq_repack_into(W4A16Weights& dst, int dst_row_offset, const uint32_t* src_packed,
+                     const __hip_bfloat16* src_scale, const uint32_t* src_zp, int out_f,
+                     hipStream_t stream = 0);
+// AWQ-order sources (layout QW4_LAYOUT_AWQ_K or QW4_LAYOUT_AWQ_N); no reference
+// counterpart.
+void awq_repack_awq_into(W4A16Weights& dst, int dst_row_offset, const uint32_t* qweight,
+                         const __hip_bfloat16* scales, const uint32_t* zeros, int out_f,
+                         int layout, hipStream_t stream = 0);
+void awq_free(W4A16Weights& w);
+
+struct GemvScratch {
+  float* partial = nullptr;   // split-K accumulation area (partial_elems floats)
+  size_t partial_elems = 0;
+  int max_in = 0, max_out = 0, max_m = 1;
+  qw4_scratch impl{};         // the C-ABI scratch these fields mirror
+};
+
+void gemv_scratch_alloc(GemvScratch& s, int max_in, int max_out, int min_group, int max_m = 1);
+void gemv_scratch_free(GemvScratch& s);
+void gemv_partial_check(const GemvScratch& s, int splits, int out_f, int M);
+size_t gemv_scratch_bytes_for_m(const GemvScratch& s, int max_m);
+
+void gemm_small_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int M,
+                      GemvScratch& s, hipStream_t stream = 0);
+void gemv_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x,
+                GemvScratch& s, hipStream_t stream = 0);
+void gemv_w4a16_f32(float* y, const W4A16Weights& w, const __hip_bfloat16* x, GemvScratch& s,
+                    hipStream_t stream = 0);
+int gemv_choose_splits(int out_f, int num_groups);
+void gemm_mma_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int M,
+                    GemvScratch& s, hipStream_t stream = 0);
+// lm_head GEMV + fused fp32 row-argmax (head() + argmax, model.cu:796-815).
+void gemv_argmax_w4a16(int32_t* idx, const W4A16Weights& w, const __hip_bfloat16* x, int M,
+                       GemvScratch& s, hipStream_t stream = 0);
+
+struct GemmWorkspace {
+  __hip_bfloat16* wbuf = nullptr;
+  size_t bytes = 0;
+  int max_rows = 0;
+};
+
+void gemm_workspace_alloc(GemmWorkspace& ws, size_t bytes);
+void gemm_workspace_free(GemmWorkspace& ws);
+void gemm_w4a16(__hip_bfloat16* C, const W4A16Weights& w, const __hip_bfloat16* A, int M,
+                GemmWorkspace& ws, hipStream_t stream = 0);
+void w4a16_dequant_rows(__hip_bfloat16* dst, const W4A16Weights& w, int row0, int nrows,
+                        hipStream_t stream = 0);
+
+void argmax(int32_t* out, const __hip_bfloat16* x, int n, int32_t* scratch,
+            hipStream_t stream = 0);
+void argmax_rows(int32_t* out, const __hip_bfloat16* x, int rows, int n, hipStream_t stream = 0);
+
+}  // namespace qwen

@@ -101,3 +101,15 @@ def test_choose_splits(hip):
                  (64, 4), (64, 136)):
         s = hip.gemv_choose_splits(n, g)
         assert 1 <= s <= max(1, (n // 64) * g // 4) + 1
+
+
+def test_cpp_layer_exports_every_declared_function(hip):
+    """include/qwen_w4a16.hpp (the reference-compatible namespace qwen layer):
+    every declared function is defined in the library."""
+    import subprocess
+
+    text = re.sub(r"//.*", "", open(os.path.join(ROOT, "include", "qwen_w4a16.hpp")).read())
+    names = set(re.findall(r"^(?:void|int|size_t)\s+([a-z_0-9]+)\s*\(", text, flags=re.M))
+    out = subprocess.run(["nm", "-DC", hip.LIB_PATH], capture_output=True, text=True).stdout
+    defined = set(re.findall(r" T qwen::([a-z_0-9]+)\(", out))
+    assert len(names) >= 20 and names <= defined, names - defined
