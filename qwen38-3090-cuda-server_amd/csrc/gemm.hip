@@ -14,6 +14,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 
 #include "../../include/qwen_w4a16.h"
@@ -163,6 +164,214 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
     }
 }
 
+
+// ---------------------------------------------------------------------------
+// k_gemm2: 256 (M) x 256 (N) workgroup tile, 8 waves (two per SIMD), each wave
+// one 32-row half of a 64-row weight tile against all 256 activation rows,
+// v_mfma_f32_32x32x16_bf16 (the full-rate bf16 shape on gfx950).
+//
+//  * Weights are the MFMA A operand (rows = output columns n). Each wave loads
+//    its packed rows straight into registers -- 32 B per lane per group, one
+//    group ahead -- and dequantizes them in registers to exactly
+//    RNE((q - z) * s): every weight element is converted once per workgroup
+//    and never touches LDS.
+//  * Activations are the B operand. A group's 256 x 128 activation tile goes
+//    global -> LDS directly (global_load_lds_dwordx4), double-buffered, one
+//    instruction per 4 full rows (1 KiB, fully coalesced). LDS row m holds
+//    16-byte chunk c of the row at slot c ^ (m % 16): lane i of a load
+//    instruction writes slot i % 16 and so fetches chunk (i % 16) ^ (m % 16)
+//    (the XOR keeps each 4-lane group inside one 64-byte sector). The MFMA
+//    operand reads (32 rows x 16 B per half-wave) then hit distinct banks.
+//  * k permutation: lane l (row r = l % 32, half h = l / 32) of k-step (s, t)
+//    holds k = 64 s + 32 h + 8 t + e -- word t of chunk 2 s + h of its weight
+//    row -- and reads the activation chunk 8 s + 4 h + t, the same k.
+//  * Row permutation: MFMA row r of tile half b reads tile position
+//    p = 16 (r % 4) + 8 b + 2 (r / 8) + (r / 4) % 2, so the four D rows a lane
+//    holds for each r / 8 are four consecutive output columns: one 8-byte
+//    store.
+constexpr int G2_BM = 256, G2_BN = 256, G2_MB = G2_BM / 32, G2_WAVES = 8;
+constexpr int G2_ROWBLOCKS = G2_BM / 4;  // 1 KiB (4-row) activation loads per group
+
+typedef float f32x16v __attribute__((ext_vector_type(16)));
+
+struct Gemm2Args {
+  const uint32_t* qw;
+  const uint16_t* sc;
+  const uint16_t* zr;
+  const uint16_t* A;
+  uint16_t* C;
+  int M, N, K, G, tiles_n;
+};
+
+// NH = 1: a wave owns one 32-row tile half against all 8 m-blocks;
+// NH = 2: a wave owns a whole 64-row tile against 4 m-blocks (half the LDS
+// reads per MFMA, every weight dequantized by two waves).
+template <int NH>
+struct WeightGroup {
+  u32x4 q[NH][2];    // [half][s]: chunk 2 s + h of this lane's weight row
+  uint32_t s[NH];    // scale bits
+  uint32_t z[NH];    // zero-point word (4 rows, 4 bits each)
+};
+
+// Unconditional loads (an out-of-range wave reads the last tile and stores
+// nothing), and the zero-point word is kept raw: arithmetic on a loaded value
+// here would make the compiler wait for every earlier load, including the
+// activation loads just issued.
+template <int NH>
+__device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const Gemm2Args& a,
+                                                int tile, int b0, int g, int lane) {
+  const int r = lane & 31, h = lane >> 5;
+  const size_t blk = (size_t)tile * a.G + g;
+#pragma unroll
+  for (int j = 0; j < NH; ++j) {
+    const int a16 = 8 * (b0 + j) + 2 * (r >> 3) + ((r >> 2) & 1);   // position % 16
+    const int p = 16 * (r & 3) + a16;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+      wg.q[j][s] = *reinterpret_cast<const u32x4*>(a.qw + blk * kWordsPerBlock +
+                                                   (2 * s + h) * 256 + p * 4);
+    wg.s[j] = a.sc[blk * 64 + 4 * a16 + (r & 3)];
+    wg.z[j] = a.zr[blk * 16 + a16];
+  }
+}
+
+// Issue this wave's share of the activation rows of group g into buf.
+__device__ __forceinline__ void g2_load_act(const Gemm2Args& a, u32x4* buf, int m0, int g,
+                                            int wave, int lane) {
+  constexpr int per_wave = G2_ROWBLOCKS / G2_WAVES;
+#pragma unroll
+  for (int i = 0; i < per_wave; ++i) {
+    const int rb = wave * per_wave + i;
+    const int row = 4 * rb + (lane >> 4);
+    const int c = (lane & 15) ^ (row & 15);
+    const int m = min(m0 + row, a.M - 1);
+    const uint16_t* src = a.A + (size_t)m * a.K + g * kGroup + 8 * c;
+    __builtin_amdgcn_global_load_lds(src, buf + rb * 64, 16, 0, 0);
+  }
+}
+
+__device__ __forceinline__ bf16x8 g2_deq(uint32_t w, float s, float c, NibConst kc) {
+#if QW4_G2_DIAG & 8
+  return __builtin_bit_cast(bf16x8, u32x4{w, w ^ 1u, w ^ 2u, w ^ 3u});
+#endif
+  const u32x4 m = nib8_bits(w, kc);
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float lo = __uint_as_float(m[i] << 16);
+    const float hi = __uint_as_float(m[i] & 0xffff0000u);
+    o[i] = pack_bf16x2(__builtin_fmaf(lo, s, c), __builtin_fmaf(hi, s, c));
+  }
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void g2_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+template <int NH>
+__global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
+  constexpr int MBW = G2_MB / NH;           // m-blocks per wave
+  __shared__ u32x4 lds[2][G2_BM * 16];   // 2 x 64 KiB: [row][16 swizzled chunks]
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
+  const int tn = blockIdx.x % a.tiles_n, tm = blockIdx.x / a.tiles_n;
+  const int m0 = tm * G2_BM;
+  const int tile = tn * 4 + (NH == 1 ? (wave >> 1) : (wave & 3));
+  const int b0 = NH == 1 ? (wave & 1) : 0;
+  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;   // first m-block of this wave
+  const bool valid = tile * kTileN < a.N;
+  const int ltile = valid ? tile : (a.N / kTileN - 1);
+
+  f32x16v acc[NH][MBW];
+#pragma unroll
+  for (int j = 0; j < NH; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) acc[j][mb] = f32x16v{};
+
+  const NibConst kc = nib_const();
+  const int zsh = 4 * (r & 3);
+  WeightGroup<NH> cur, nxt;
+  g2_load_act(a, lds[0], m0, 0, wave, lane);
+  g2_load_weights(cur, a, ltile, b0, 0, lane);
+  for (int g = 0; g < a.G; ++g) {
+    g2_wait_vm0();
+    __syncthreads();
+    const u32x4* buf = lds[g & 1] + (32 * mw + r) * 16;
+    if (g + 1 < a.G) {
+#if !(QW4_G2_DIAG & 1)
+      g2_load_act(a, lds[(g + 1) & 1], m0, g + 1, wave, lane);
+#endif
+#if !(QW4_G2_DIAG & 2)
+      g2_load_weights(nxt, a, ltile, b0, g + 1, lane);
+#else
+      nxt = cur;
+#endif
+    }
+    float sf[NH], cf[NH];
+#pragma unroll
+    for (int j = 0; j < NH; ++j) {
+      sf[j] = bf16_bits_to_f32(cur.s[j]);
+      cf[j] = -(128.0f + (float)((cur.z[j] >> zsh) & 0xFu)) * sf[j];
+    }
+    // Software pipeline over the group's 8 k-steps: the activation operands
+    // and the dequantized weight operands of step u + 1 are produced while
+    // step u's MFMAs run.
+    u32x4 xo[2][MBW];
+    bf16x8 wd[2][NH];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) xo[0][mb] = buf[mb * 512 + ((4 * h) ^ (r & 15))];
+#pragma unroll
+    for (int j = 0; j < NH; ++j) wd[0][j] = g2_deq(cur.q[j][0][0], sf[j], cf[j], kc);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int cu = u & 1, nu = cu ^ 1;
+      if (u + 1 < 8) {
+        const int s1 = (u + 1) >> 2, t1 = (u + 1) & 3;
+        const int slot = (8 * s1 + 4 * h + t1) ^ (r & 15);
+#pragma unroll
+        for (int mb = 0; mb < MBW; ++mb) xo[nu][mb] = buf[mb * 512 + slot];
+#pragma unroll
+        for (int j = 0; j < NH; ++j) wd[nu][j] = g2_deq(cur.q[j][s1][t1], sf[j], cf[j], kc);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+        for (int j = 0; j < NH; ++j)
+          acc[j][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              wd[cu][j], __builtin_bit_cast(bf16x8, xo[cu][mb]), acc[j][mb], 0, 0, 0);
+#ifndef QW4_G2_NOSCHED
+      if (u + 1 < 8) {
+#pragma unroll
+        for (int i = 0; i < MBW * NH; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (i < MBW / 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x002, 4 * NH, 0);  // VALU
+        }
+      }
+#endif
+    }
+    cur = nxt;
+  }
+
+  if (!valid) return;
+  // D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
+  // columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
+#pragma unroll
+  for (int mb = 0; mb < MBW; ++mb) {
+    const int m = m0 + 32 * (mw + mb) + r;
+    if (m >= a.M) continue;
+    uint16_t* crow = a.C + (size_t)m * a.N + tile * kTileN;
+#pragma unroll
+    for (int j = 0; j < NH; ++j)
+#pragma unroll
+      for (int jq = 0; jq < 4; ++jq) {
+        const u32x2 o = {pack_bf16x2(acc[j][mb][4 * jq], acc[j][mb][4 * jq + 1]),
+                         pack_bf16x2(acc[j][mb][4 * jq + 2], acc[j][mb][4 * jq + 3])};
+        *reinterpret_cast<u32x2*>(crow + 4 * (8 * (b0 + j) + 2 * jq + h)) = o;
+      }
+  }
+}
+
 }  // namespace
 }  // namespace qw4
 
@@ -200,6 +409,25 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
   if (!C || !A) return QW4_ERR_NULL;
   if (M < 1) return QW4_ERR_M;
   if (((uintptr_t)A & 15) || ((uintptr_t)C & 1)) return QW4_ERR_ALIGN;
+  static const int version = [] {
+    const char* e = std::getenv("QW4_GEMM_V");
+    return e ? std::atoi(e) : 2;
+  }();
+  if (version == 2) {
+    if (((uintptr_t)C & 7)) return QW4_ERR_ALIGN;
+    const int tiles_n = (w->out_f + G2_BN - 1) / G2_BN;
+    Gemm2Args a{w->qweight, w->scale, w->zeros, A, C, M, w->out_f, w->in_f, w->num_groups,
+                tiles_n};
+    const int grid = ((M + G2_BM - 1) / G2_BM) * tiles_n;
+    static const int nh = [] {
+      const char* e = std::getenv("QW4_GEMM_NH");
+      return e ? std::atoi(e) : 1;
+    }();
+    if (nh == 2) k_gemm2<2><<<grid, 512, 0, (hipStream_t)stream>>>(a);
+    else k_gemm2<1><<<grid, 512, 0, (hipStream_t)stream>>>(a);
+    QW4_LAUNCH_CHECK();
+    return QW4_OK;
+  }
   GemmArgs a{w->qweight, w->scale, w->zeros, A, C, M, w->out_f, w->in_f, w->num_groups};
   const int grid = ((M + BM - 1) / BM) * ((w->out_f + BN - 1) / BN);
   k_gemm<<<grid, 256, 0, (hipStream_t)stream>>>(a);
