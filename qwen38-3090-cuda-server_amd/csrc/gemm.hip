@@ -200,7 +200,9 @@ struct Gemm2Args {
   const uint16_t* zr;
   const uint16_t* A;
   uint16_t* C;
-  int M, N, K, G, tiles_n;
+  float* slots;         // stream-K: [P][2] fp32 partial tiles
+  int M, N, K, G, tiles_n, tiles_m, map;
+  int P, U;             // workgroups, (tile, group) units
 };
 
 // NH = 1: a wave owns one 32-row tile half against all 8 m-blocks;
@@ -213,40 +215,47 @@ struct WeightGroup {
   uint32_t z[NH];    // zero-point word (4 rows, 4 bits each)
 };
 
-// Unconditional loads (an out-of-range wave reads the last tile and stores
-// nothing), and the zero-point word is kept raw: arithmetic on a loaded value
-// here would make the compiler wait for every earlier load, including the
+// Buffer-resource addressing: a 32-bit per-lane offset (loop-invariant) plus
+// a scalar offset, instead of a 64-bit address per lane and load. Loads are
+// unconditional (an out-of-range wave reads the last tile and stores nothing),
+// and the zero-point word is kept raw: arithmetic on a loaded value here
+// would make the compiler wait for every earlier load, including the
 // activation loads just issued.
+struct G2Rsrc {
+  __amdgpu_buffer_rsrc_t qw, sc, zr;
+};
+
 template <int NH>
-__device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const Gemm2Args& a,
+__device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const G2Rsrc& rs, int G,
                                                 int tile, int b0, int g, int lane) {
   const int r = lane & 31, h = lane >> 5;
-  const size_t blk = (size_t)tile * a.G + g;
+  const uint32_t blk = (uint32_t)tile * (uint32_t)G + (uint32_t)g;   // < 2^26
 #pragma unroll
   for (int j = 0; j < NH; ++j) {
     const int a16 = 8 * (b0 + j) + 2 * (r >> 3) + ((r >> 2) & 1);   // position % 16
     const int p = 16 * (r & 3) + a16;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
-      wg.q[j][s] = *reinterpret_cast<const u32x4*>(a.qw + blk * kWordsPerBlock +
-                                                   (2 * s + h) * 256 + p * 4);
-    wg.s[j] = a.sc[blk * 64 + 4 * a16 + (r & 3)];
-    wg.z[j] = a.zr[blk * 16 + a16];
+      wg.q[j][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.qw, ((2 * s + h) * 64 + p) * 16,
+                                                         blk * 4096u, 0);
+    wg.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (4 * a16 + (r & 3)) * 2, blk * 128u, 0);
+    wg.z[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.zr, a16 * 2, blk * 32u, 0);
   }
 }
 
-// Issue this wave's share of the activation rows of group g into buf.
-__device__ __forceinline__ void g2_load_act(const Gemm2Args& a, u32x4* buf, int m0, int g,
-                                            int wave, int lane) {
+// Issue this wave's share of the activation rows of group g into buf. `act`
+// covers rows [m0, M) of A; rows past M lie outside it and read as zeros.
+// voff[i % 4] is the lane's byte offset of instruction i relative to its
+// first row (the swizzle repeats every 4 instructions).
+__device__ __forceinline__ void g2_load_act(__amdgpu_buffer_rsrc_t act, const uint32_t (&voff)[4],
+                                            uint32_t row_bytes, u32x4* buf, int g, int wave) {
   constexpr int per_wave = G2_ROWBLOCKS / G2_WAVES;
 #pragma unroll
   for (int i = 0; i < per_wave; ++i) {
     const int rb = wave * per_wave + i;
-    const int row = 4 * rb + (lane >> 4);
-    const int c = (lane & 15) ^ (row & 15);
-    const int m = min(m0 + row, a.M - 1);
-    const uint16_t* src = a.A + (size_t)m * a.K + g * kGroup + 8 * c;
-    __builtin_amdgcn_global_load_lds(src, buf + rb * 64, 16, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(act, buf + rb * 64, 16,
+                                             voff[i & 3] + (uint32_t)(4 * rb) * row_bytes,
+                                             (uint32_t)g * (kGroup * 2), 0, 0);
   }
 }
 
@@ -268,41 +277,66 @@ __device__ __forceinline__ bf16x8 g2_deq(uint32_t w, float s, float c, NibConst 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void g2_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
-template <int NH>
-__global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
-  constexpr int MBW = G2_MB / NH;           // m-blocks per wave
-  __shared__ u32x4 lds[2][G2_BM * 16];   // 2 x 64 KiB: [row][16 swizzled chunks]
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int r = lane & 31, h = lane >> 5;
-  const int tn = blockIdx.x % a.tiles_n, tm = blockIdx.x / a.tiles_n;
-  const int m0 = tm * G2_BM;
-  const int tile = tn * 4 + (NH == 1 ? (wave >> 1) : (wave & 3));
-  const int b0 = NH == 1 ? (wave & 1) : 0;
-  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;   // first m-block of this wave
-  const bool valid = tile * kTileN < a.N;
-  const int ltile = valid ? tile : (a.N / kTileN - 1);
+// Linear tile index -> (tn, tm), in bands of 4 M-tiles: consecutive tiles
+// share an activation tile (and, 4 apart, a weight tile), so the ~32
+// workgroups an XCD runs at once touch ~4 activation and ~8 weight tiles.
+__device__ __forceinline__ void g2_tile_coords(const Gemm2Args& a, int t, int& tn, int& tm) {
+  const int band = 4 * a.tiles_n;
+  const int b = t / band, w = t % band;
+  const int rows = min(4, a.tiles_m - 4 * b);
+  tm = 4 * b + w % rows;
+  tn = w / rows;
+}
 
-  f32x16v acc[NH][MBW];
+// Workgroups are dealt round-robin to the 8 XCDs (each with its own L2): XCD x
+// runs blocks x, x + 8, ... Renumber so that each XCD owns a contiguous run of
+// work. Needs count % 8 == 0 (then it is a bijection).
+__device__ __forceinline__ int g2_xcd_order(int blk, int count) {
+  return (blk & 7) * (count >> 3) + (blk >> 3);
+}
+
+// One wave's share of one (tile, group range) segment: acc = sum over groups
+// [g0, g1) of this wave's weight rows x the tile's activation rows.
+template <int NH>
+__device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
+                                           u32x4 (*lds)[G2_BM * 16],
+                                           f32x16v (&acc)[NH][G2_MB / NH], int m0, int ltile,
+                                           int b0, int mw, int g0, int g1, int wave,
+                                           int lane, NibConst kc) {
+  constexpr int MBW = G2_MB / NH;
+  const int r = lane & 31, h = lane >> 5;
+  const int zsh = 4 * (r & 3);
 #pragma unroll
   for (int j = 0; j < NH; ++j)
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) acc[j][mb] = f32x16v{};
-
-  const NibConst kc = nib_const();
-  const int zsh = 4 * (r & 3);
   WeightGroup<NH> cur, nxt;
-  g2_load_act(a, lds[0], m0, 0, wave, lane);
-  g2_load_weights(cur, a, ltile, b0, 0, lane);
-  for (int g = 0; g < a.G; ++g) {
+  // Activation rows [m0, M): the buffer's end turns rows past M into zeros.
+  const uint32_t row_bytes = (uint32_t)a.K * 2u;
+  const __amdgpu_buffer_rsrc_t act = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.A) + (size_t)m0 * a.K, 0, (int)((uint32_t)(a.M - m0) * row_bytes),
+      0x00020000);
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 4 * i + (lane >> 4);                 // row within the 16-row swizzle period
+    const int c = (lane & 15) ^ (row & 15);
+    voff[i] = (uint32_t)(lane >> 4) * row_bytes + (uint32_t)c * 16u;
+  }
+  __syncthreads();   // the previous segment's last LDS reads are done
+  g2_load_act(act, voff, row_bytes, lds[0], g0, wave);
+  g2_load_weights(cur, rs, a.G, ltile, b0, g0, lane);
+  for (int g = g0; g < g1; ++g) {
     g2_wait_vm0();
     __syncthreads();
-    const u32x4* buf = lds[g & 1] + (32 * mw + r) * 16;
-    if (g + 1 < a.G) {
+    const int sb = (g - g0) & 1;
+    const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
+    if (g + 1 < g1) {
 #if !(QW4_G2_DIAG & 1)
-      g2_load_act(a, lds[(g + 1) & 1], m0, g + 1, wave, lane);
+      g2_load_act(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave);
 #endif
 #if !(QW4_G2_DIAG & 2)
-      g2_load_weights(nxt, a, ltile, b0, g + 1, lane);
+      g2_load_weights(nxt, rs, a.G, ltile, b0, g + 1, lane);
 #else
       nxt = cur;
 #endif
@@ -322,6 +356,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
     for (int mb = 0; mb < MBW; ++mb) xo[0][mb] = buf[mb * 512 + ((4 * h) ^ (r & 15))];
 #pragma unroll
     for (int j = 0; j < NH; ++j) wd[0][j] = g2_deq(cur.q[j][0][0], sf[j], cf[j], kc);
+    // Fence: the prologue's reads must not fill the DS slots of the pattern below.
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int cu = u & 1, nu = cu ^ 1;
@@ -352,10 +388,15 @@ __global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
     }
     cur = nxt;
   }
+}
 
-  if (!valid) return;
-  // D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
-  // columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
+// D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
+// columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
+template <int NH>
+__device__ __forceinline__ void g2_store(const Gemm2Args& a, const f32x16v (&acc)[NH][G2_MB / NH],
+                                         int m0, int tile, int b0, int mw, int lane) {
+  constexpr int MBW = G2_MB / NH;
+  const int r = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
     const int m = m0 + 32 * (mw + mb) + r;
@@ -370,6 +411,150 @@ __global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
         *reinterpret_cast<u32x2*>(crow + 4 * (8 * (b0 + j) + 2 * jq + h)) = o;
       }
   }
+}
+
+// Stream-K partial tiles. Each workgroup has two fp32 slots (for its first
+// and its last tile), laid out [wave][m-block][lane] in 64-byte runs. A
+// workgroup whose range cuts a tile writes its partial there; a second kernel
+// (k_gemm2_fixup, stream-ordered after this one) sums each cut tile's slots in
+// workgroup order -- a fixed order, so results are bitwise reproducible -- and
+// stores the tile.
+constexpr uint32_t kSlotBytes = (uint32_t)G2_BM * G2_BN * 4;   // 256 KiB
+
+__device__ __forceinline__ uint32_t g2_slot_off(int vp, int which, int wave, int mb, int lane) {
+  return (uint32_t)(vp * 2 + which) * kSlotBytes +
+         (uint32_t)(((wave * G2_MB + mb) * 64 + lane) * 64);
+}
+
+template <int NH>
+__device__ __forceinline__ void g2_slot_store(__amdgpu_buffer_rsrc_t rs,
+                                              const f32x16v (&acc)[NH][G2_MB / NH], int vp,
+                                              int which, int wave, int lane) {
+  constexpr int MBW = G2_MB / NH;
+#pragma unroll
+  for (int j = 0; j < NH; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) {
+      const uint32_t off = g2_slot_off(vp, which, wave, j * MBW + mb, lane);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = {__float_as_uint(acc[j][mb][4 * i]), __float_as_uint(acc[j][mb][4 * i + 1]),
+                         __float_as_uint(acc[j][mb][4 * i + 2]),
+                         __float_as_uint(acc[j][mb][4 * i + 3])};
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, off + 16 * i, 0, 0);
+      }
+    }
+}
+
+__device__ __forceinline__ int g2_range_start(const Gemm2Args& a, int vp) {
+  return (int)((long long)vp * a.U / a.P);
+}
+// Largest vp with g2_range_start(vp) <= u.
+__device__ __forceinline__ int g2_owner_of(const Gemm2Args& a, int u) {
+  return (int)(((long long)(u + 1) * a.P - 1) / a.U);
+}
+
+// One workgroup per tile (8 waves, the main kernel's wave -> row mapping);
+// tiles that a single workgroup covered were stored by the main kernel.
+template <int NH>
+__global__ __launch_bounds__(512) void k_gemm2_fixup(Gemm2Args a) {
+  constexpr int MBW = G2_MB / NH;
+  const int t = blockIdx.x;
+  const int p0 = g2_owner_of(a, t * a.G), p1 = g2_owner_of(a, t * a.G + a.G - 1);
+  if (p0 == p1) return;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int wt = NH == 1 ? (wave >> 1) : (wave & 3);
+  const int b0 = NH == 1 ? (wave & 1) : 0;
+  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;
+  int tn, tm;
+  g2_tile_coords(a, t, tn, tm);
+  const int tile = tn * 4 + wt;
+  if (tile * kTileN >= a.N) return;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)(2u * a.P * kSlotBytes), 0x00020000);
+  f32x16v acc[NH][MBW];
+#pragma unroll
+  for (int j = 0; j < NH; ++j)
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb) acc[j][mb] = f32x16v{};
+  for (int pp = p0; pp <= p1; ++pp) {
+    const int which = (g2_range_start(a, pp) / a.G == t) ? 0 : 1;
+#pragma unroll
+    for (int j = 0; j < NH; ++j)
+#pragma unroll
+      for (int mb = 0; mb < MBW; ++mb) {
+        const uint32_t off = g2_slot_off(pp, which, wave, j * MBW + mb, lane);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[j][mb][4 * i + e] += __uint_as_float(v[e]);
+        }
+      }
+  }
+  g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+}
+
+template <int NH>
+__global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
+  constexpr int MBW = G2_MB / NH;           // m-blocks per wave
+  __shared__ u32x4 lds[2][G2_BM * 16];      // 2 x 64 KiB: [row][16 swizzled chunks]
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int wt = NH == 1 ? (wave >> 1) : (wave & 3);   // tile of the 4 this wave owns
+  const int b0 = NH == 1 ? (wave & 1) : 0;
+  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;      // first m-block of this wave
+  const NibConst kc = nib_const();
+  f32x16v acc[NH][MBW];
+
+  // Virtual workgroup vp owns units [start(vp), start(vp + 1)) of the
+  // U = tiles x G (tile, group) units; XCD x owns a contiguous run of vp. With
+  // P = tiles (U / P = G) every range is exactly one whole tile; with P = CUs
+  // ranges cut tiles (stream-K) and the cut tiles are combined through slots.
+  const int vp = a.map ? g2_xcd_order(blockIdx.x, a.P) : (int)blockIdx.x;
+  const int u0 = g2_range_start(a, vp), u1 = g2_range_start(a, vp + 1);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)(2u * a.P * kSlotBytes), 0x00020000);
+  G2Rsrc wr;
+  wr.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0,
+                                            (int)((uint32_t)a.N * (uint32_t)a.K / 2u), 0x00020000);
+  wr.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0,
+                                            (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
+  wr.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
+                                            (int)((uint32_t)a.N * (uint32_t)a.G / 2u), 0x00020000);
+  for (int u = u0; u < u1;) {
+    const int t = u / a.G, g0 = u - t * a.G;
+    const int g1 = min(a.G, u1 - t * a.G);
+    int tn, tm;
+    g2_tile_coords(a, t, tn, tm);
+    const int tile = tn * 4 + wt;
+    const bool valid = tile * kTileN < a.N;
+    const int ltile = valid ? tile : (a.N / kTileN - 1);
+    g2_segment<NH>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane, kc);
+    if (g0 == 0 && g1 == a.G) {
+      if (valid) g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+    } else {
+      g2_slot_store<NH>(rs, acc, vp, u == u0 ? 0 : 1, wave, lane);
+    }
+    u = t * a.G + g1;
+  }
+}
+
+// Workspace bytes that enable stream-K: two fp32 partial tiles per CU.
+size_t gemm_workspace_need(int cus) { return 2ull * (size_t)cus * kSlotBytes; }
+
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
 }
 
 }  // namespace
@@ -403,7 +588,6 @@ int qw4_workspace_free(qw4_workspace* ws) {
 
 int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_workspace* ws,
              void* stream) {
-  (void)ws;
   int st = check_weights_public(w);
   if (st) return st;
   if (!C || !A) return QW4_ERR_NULL;
@@ -416,15 +600,49 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
   if (version == 2) {
     if (((uintptr_t)C & 7)) return QW4_ERR_ALIGN;
     const int tiles_n = (w->out_f + G2_BN - 1) / G2_BN;
-    Gemm2Args a{w->qweight, w->scale, w->zeros, A, C, M, w->out_f, w->in_f, w->num_groups,
-                tiles_n};
-    const int grid = ((M + G2_BM - 1) / G2_BM) * tiles_n;
+    const int tiles_m = (M + G2_BM - 1) / G2_BM;
+    static const int map_env = [] {
+      const char* e = std::getenv("QW4_GEMM_MAP");
+      return e ? std::atoi(e) : 1;
+    }();
+    const int nt = tiles_n * tiles_m;
+    Gemm2Args a{w->qweight, w->scale, w->zeros, A, C, nullptr, M, w->out_f, w->in_f,
+                w->num_groups, tiles_n, tiles_m, map_env && nt % 8 == 0, nt, nt * w->num_groups};
+    int grid = nt;
+    // Stream-K (one workgroup per CU, the (tile, group) units split evenly)
+    // when it beats one workgroup per tile by a margin. Costs in group-steps
+    // per CU: whole tiles take ceil(nt / CUs) * G; stream-K takes nt * G / CUs
+    // plus ~16 for writing and re-reading the cut tiles' fp32 partials.
+    static const int sk_env = [] {
+      const char* e = std::getenv("QW4_GEMM_SK");
+      return e ? std::atoi(e) : -1;   // -1: by the cost model, 0: never, 1: always
+    }();
+    const int cus = device_cus();
+    const long long G = w->num_groups;
+    const double t_dp = (double)((nt + cus - 1) / cus) * G;
+    const double t_sk = (double)nt * G / cus + 16.0;
+    const bool sk_ok = ws && ws->buf && ws->bytes >= gemm_workspace_need(cus) &&
+                       cus % 8 == 0 && nt % cus != 0 && (long long)nt * G >= 2LL * cus &&
+                       (long long)nt * G < (1LL << 31);
+    if (sk_ok && (sk_env == 1 || (sk_env == -1 && t_sk < 0.9 * t_dp))) {
+      a.slots = static_cast<float*>(ws->buf);
+      a.P = cus;
+      a.U = (int)(nt * G);
+      a.map = 1;
+      grid = cus;
+    }
     static const int nh = [] {
       const char* e = std::getenv("QW4_GEMM_NH");
       return e ? std::atoi(e) : 1;
     }();
-    if (nh == 2) k_gemm2<2><<<grid, 512, 0, (hipStream_t)stream>>>(a);
-    else k_gemm2<1><<<grid, 512, 0, (hipStream_t)stream>>>(a);
+    hipStream_t s = (hipStream_t)stream;
+    if (nh == 2) k_gemm2<2><<<grid, 512, 0, s>>>(a);
+    else k_gemm2<1><<<grid, 512, 0, s>>>(a);
+    QW4_LAUNCH_CHECK();
+    if (grid != nt) {
+      if (nh == 2) k_gemm2_fixup<2><<<nt, 512, 0, s>>>(a);
+      else k_gemm2_fixup<1><<<nt, 512, 0, s>>>(a);
+    }
     QW4_LAUNCH_CHECK();
     return QW4_OK;
   }

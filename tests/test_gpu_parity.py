@@ -227,20 +227,39 @@ def test_lm_head_argmax(hip, orc, scratch, N, M):
 
 
 # ----------------------------------------------------------------- prefill
+@pytest.fixture(scope="module")
+def gemm_ws(hip):
+    """A prefill workspace as the reference sizes it (256 MiB, model.cu:440); with
+    it the GEMM may split tiles across workgroups (stream-K)."""
+    ws = hip.gemm_workspace_alloc(256 << 20)
+    yield ws
+    hip.gemm_workspace_free(ws)
+
+
 @pytest.mark.parametrize("M,N,K", [(1, 128, 512), (77, 320, 1024), (512, 17408, 5120),
-                                   (512, 5120, 17408), (200, 5184, 1536)])
-def test_prefill_gemm_vs_oracle(hip, orc, M, N, K):
+                                   (512, 5120, 17408), (200, 5184, 1536), (777, 5184, 4096)])
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     """BASELINE config 4 semantics: RNE(bf16) dequant, fp32 accumulation, bf16 out.
     The oracle is evaluated on a sample of rows of A (each output row depends only
-    on its own row of A)."""
+    on its own row of A). With a workspace, shapes whose tiles do not fill the
+    chip evenly run stream-K (tiles cut across workgroups, partials combined in
+    a fixed order): checked against the oracle and bitwise against the
+    one-workgroup-per-tile result."""
     import torch
 
     q, zp, s = orc.gen_weights(N, K, seed=M)
     x = orc.gen_x(M, K, seed=M)
     w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
     y = empty((M, N), np.uint16)
-    hip.gemm_w4a16(y, w, dev(x), M)
+    dx = dev(x)
+    hip.gemm_w4a16(y, w, dx, M, gemm_ws if use_ws else None)
     torch.cuda.synchronize()
+    if use_ws:
+        y1 = empty((M, N), np.uint16)
+        hip.gemm_w4a16(y1, w, dx, M, gemm_ws)   # the counters reset themselves
+        torch.cuda.synchronize()
+        assert torch.equal(y, y1), "stream-K result not reproducible"
     rows = np.unique(np.r_[0, M - 1, np.random.default_rng(M).integers(0, M, 14)])
     ref = orc.matmul_f64(x[rows], q, zp, s, round_w=True)
     _check_bf16(orc, host(y, np.uint16)[rows], ref, f"prefill {M}x{N}x{K}")
@@ -248,7 +267,7 @@ def test_prefill_gemm_vs_oracle(hip, orc, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(4096, 17408, 5120), (4096, 5120, 17408), (1024, 17408, 5120)])
-def test_prefill_gemm_full_vs_torch_fp32(hip, orc, M, N, K):
+def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
     """Full-size prefill against a torch fp32 GEMM of the bit-exact dequantized
     weights (dequant_rows is pinned bit-exact above)."""
     import torch
@@ -262,7 +281,7 @@ def test_prefill_gemm_full_vs_torch_fp32(hip, orc, M, N, K):
     A = empty((M, K), np.uint16)
     hip.gen_bf16(A, M * K, 0, 11 * 8 + 3, 0)
     y = empty((M, N), np.uint16)
-    hip.gemm_w4a16(y, w, A, M)
+    hip.gemm_w4a16(y, w, A, M, gemm_ws)
     deq = empty((N, K), np.uint16)
     hip.w4a16_dequant_rows(deq, w, 0, N)
     torch.cuda.synchronize()
