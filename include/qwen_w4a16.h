@@ -139,8 +139,12 @@ int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M
                     qw4_scratch* s, void* stream);
 
 /* ------------------------------------------------------------- prefill
- * GemmWorkspace (src/kernels/gemm_w4a16.cuh:30-35). The fused kernel needs
- * only split-K partials; bytes may be 0 (then split-K is disabled). */
+ * GemmWorkspace (src/kernels/gemm_w4a16.cuh:30-35). The fused kernel needs no
+ * dequantized-weight buffer; a workspace of at least 2 x CUs x 256 KiB
+ * (128 MiB on MI355X; the reference allocates 256 MiB, model.cu:440) lets it
+ * split tiles across workgroups (stream-K) when whole tiles would leave CUs
+ * idle. The workspace then holds fp32 partial tiles: calls that share one must
+ * be stream-ordered. NULL or smaller: one workgroup per tile. */
 typedef struct qw4_workspace {
   void* buf;
   size_t bytes;
@@ -151,7 +155,9 @@ int qw4_workspace_alloc(qw4_workspace* ws, size_t bytes);
 int qw4_workspace_free(qw4_workspace* ws);
 /* gemm_w4a16 (gemm_w4a16.cuh:40-43; .cu:63-88): C [M][out_f] bf16 =
  * A [M][in_f] bf16 @ W^T with W dequantized to bf16 (RNE((q-zp)*s)), bf16 MFMA,
- * fp32 accumulation. Any M >= 1. */
+ * fp32 accumulation. Any M >= 1 with M * in_f * 2 < 2^32. A 16-byte aligned,
+ * C 8-byte aligned. Results are bitwise reproducible for a given shape and
+ * workspace size. */
 int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M,
              qw4_workspace* ws, void* stream);
 

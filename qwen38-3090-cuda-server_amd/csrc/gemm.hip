@@ -1,16 +1,13 @@
 // Prefill W4A16 GEMM: C [M][N] = A [M][K] @ W^T, bf16 in/out, fp32 accumulate.
 //
 // The reference dequantizes whole weight tiles to a bf16 workspace and calls
-// cublasGemmEx (src/kernels/gemm_w4a16.cu:63-88). Here the dequant is fused:
-// each K step stages the packed 4 KiB (tile, group) blocks straight from the
-// repacked layout, converts them to bf16 in registers -- exactly RNE((q-z)*s),
-// the reference's k_dequant_rows arithmetic (gemm_w4a16.cu:26-36) -- and
-// writes them into LDS next to the activation tile; bf16 MFMA
-// (v_mfma_f32_16x16x32_bf16) consumes both.
-//
-// Workgroup tile BM x BN = 128 x 128, 4 waves (2 x 2), each wave 64 x 64 =
-// 4 x 4 MFMA blocks; BK = 128 = one quantization group. Global loads for
-// step k+1 are issued before the MFMAs of step k (register double buffer).
+// cublasGemmEx (src/kernels/gemm_w4a16.cu:63-88). Here the dequant is fused
+// into one gfx950 kernel: each wave converts its packed weight rows in
+// registers to exactly RNE((q - z) * s) -- the reference's k_dequant_rows
+// arithmetic (gemm_w4a16.cu:26-36) -- and feeds them to bf16 MFMA against
+// activation tiles staged in LDS. Tiles that would leave CUs idle in a last
+// partial round are instead split across workgroups (stream-K) when a
+// workspace is given; the workspace then holds fp32 partial tiles.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -25,148 +22,8 @@ int check_weights_public(const qw4_weights* w);
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 128;
-constexpr int LDA = BK + 8;   // bf16 elements per LDS row (272 B: conflict-free b128 reads)
-
-struct GemmArgs {
-  const uint32_t* qw;
-  const uint16_t* sc;
-  const uint16_t* zr;
-  const uint16_t* A;
-  uint16_t* C;
-  int M, N, K, G;
-};
-
-struct Stage {
-  u32x4 a[8];     // 8 x 16 B of activations
-  u32x4 w[2];     // 2 x 16 B of packed weights
-  uint32_t s[2];  // scale bits of the two rows
-  uint32_t z[2];  // zero point of the two rows
-};
-
-__device__ __forceinline__ void load_stage(Stage& st, const GemmArgs& a, int m0, int n0, int g,
-                                           int tid) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int id = tid + 256 * i;
-    const int r = id >> 4, ch = id & 15;
-    const int m = m0 + r;
-    st.a[i] = m < a.M ? *reinterpret_cast<const u32x4*>(a.A + (size_t)m * a.K + g * BK + ch * 8)
-                      : u32x4{0, 0, 0, 0};
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int id = tid + 256 * i;
-    const int tile = (n0 >> 6) + (id >> 8);
-    const int within = id & 255;              // 16-byte chunk in the 4 KiB block
-    const int p = within & 63;
-    const int row = tile_row_of_pos(p);
-    if (tile * kTileN < a.N) {
-      const size_t blk = (size_t)tile * a.G + g;
-      st.w[i] = *reinterpret_cast<const u32x4*>(a.qw + blk * kWordsPerBlock + within * 4);
-      st.s[i] = a.sc[blk * 64 + row];
-      st.z[i] = (a.zr[blk * 16 + (row >> 2)] >> (4 * (row & 3))) & 0xFu;
-    } else {
-      st.w[i] = u32x4{0, 0, 0, 0};
-      st.s[i] = 0;
-      st.z[i] = 0;
-    }
-  }
-}
-
-// bf16 pair (128+q_lo, 128+q_hi) -> RNE((q - z) * s) pair, exact before rounding:
-// (128 + z) * s has at most 16 significant bits, so the fma is exact.
-__device__ __forceinline__ uint32_t deq_pair(uint32_t magic, float s, float c) {
-  const float lo = __uint_as_float(magic << 16);
-  const float hi = __uint_as_float(magic & 0xffff0000u);
-  return pack_bf16x2(__builtin_fmaf(lo, s, c), __builtin_fmaf(hi, s, c));
-}
-
-__device__ __forceinline__ void store_stage(const Stage& st, uint16_t* sA, uint16_t* sB,
-                                            int tid, NibConst kc) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int id = tid + 256 * i;
-    const int r = id >> 4, ch = id & 15;
-    *reinterpret_cast<u32x4*>(sA + r * LDA + ch * 8) = st.a[i];
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int id = tid + 256 * i;
-    const int within = id & 255;
-    const int j = within >> 6, p = within & 63;
-    const int row = (id >> 8) * kTileN + tile_row_of_pos(p);
-    const float s = bf16_bits_to_f32(st.s[i]);
-    const float c = -(128.0f + (float)st.z[i]) * s;
-    uint16_t* dst = sB + row * LDA + 32 * j;
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const u32x4 m = nib8_bits(st.w[i][w], kc);
-      *reinterpret_cast<u32x4*>(dst + 8 * w) =
-          u32x4{deq_pair(m[0], s, c), deq_pair(m[1], s, c), deq_pair(m[2], s, c),
-                deq_pair(m[3], s, c)};
-    }
-  }
-}
-
-__global__ __launch_bounds__(256) void k_gemm(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[BM * LDA];
-  __shared__ __attribute__((aligned(16))) uint16_t sB[BN * LDA];
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int ntn = (a.N + BN - 1) / BN;
-  const int m0 = (blockIdx.x / ntn) * BM, n0 = (blockIdx.x % ntn) * BN;
-  const int l16 = lane & 15, lq = lane >> 4;
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  const NibConst kc = nib_const();
-  Stage st;
-  load_stage(st, a, m0, n0, 0, tid);
-  for (int g = 0; g < a.G; ++g) {
-    store_stage(st, sA, sB, tid, kc);
-    __syncthreads();
-    if (g + 1 < a.G) load_stage(st, a, m0, n0, g + 1, tid);
-#pragma unroll
-    for (int t = 0; t < BK / 32; ++t) {
-      bf16x8 fa[4], fb[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const bf16x8*>(sA + (wm * 64 + 16 * i + l16) * LDA + 32 * t + 8 * lq);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const bf16x8*>(sB + (wn * 64 + 16 * j + l16) * LDA + 32 * t + 8 * lq);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
-    }
-    __syncthreads();
-  }
-
-  // D layout: lane holds rows 4*lq + r of block i, column l16 of block j.
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 64 + 16 * j + l16;
-      if (n >= a.N) continue;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = m0 + wm * 64 + 16 * i + 4 * lq + r;
-        if (m < a.M) a.C[(size_t)m * a.N + n] = to_bf16(acc[i][j][r]);
-      }
-    }
-}
-
-
 // ---------------------------------------------------------------------------
-// k_gemm2: 256 (M) x 256 (N) workgroup tile, 8 waves (two per SIMD), each wave
+// k_gemm: 256 (M) x 256 (N) workgroup tile, 8 waves (two per SIMD), each wave
 // one 32-row half of a 64-row weight tile against all 256 activation rows,
 // v_mfma_f32_32x32x16_bf16 (the full-rate bf16 shape on gfx950).
 //
@@ -194,7 +51,7 @@ constexpr int G2_ROWBLOCKS = G2_BM / 4;  // 1 KiB (4-row) activation loads per g
 
 typedef float f32x16v __attribute__((ext_vector_type(16)));
 
-struct Gemm2Args {
+struct GemmArgs {
   const uint32_t* qw;
   const uint16_t* sc;
   const uint16_t* zr;
@@ -260,9 +117,6 @@ __device__ __forceinline__ void g2_load_act(__amdgpu_buffer_rsrc_t act, const ui
 }
 
 __device__ __forceinline__ bf16x8 g2_deq(uint32_t w, float s, float c, NibConst kc) {
-#if QW4_G2_DIAG & 8
-  return __builtin_bit_cast(bf16x8, u32x4{w, w ^ 1u, w ^ 2u, w ^ 3u});
-#endif
   const u32x4 m = nib8_bits(w, kc);
   u32x4 o;
 #pragma unroll
@@ -280,7 +134,7 @@ __device__ __forceinline__ void g2_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F7
 // Linear tile index -> (tn, tm), in bands of 4 M-tiles: consecutive tiles
 // share an activation tile (and, 4 apart, a weight tile), so the ~32
 // workgroups an XCD runs at once touch ~4 activation and ~8 weight tiles.
-__device__ __forceinline__ void g2_tile_coords(const Gemm2Args& a, int t, int& tn, int& tm) {
+__device__ __forceinline__ void g2_tile_coords(const GemmArgs& a, int t, int& tn, int& tm) {
   const int band = 4 * a.tiles_n;
   const int b = t / band, w = t % band;
   const int rows = min(4, a.tiles_m - 4 * b);
@@ -298,7 +152,7 @@ __device__ __forceinline__ int g2_xcd_order(int blk, int count) {
 // One wave's share of one (tile, group range) segment: acc = sum over groups
 // [g0, g1) of this wave's weight rows x the tile's activation rows.
 template <int NH>
-__device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
+__device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
                                            u32x4 (*lds)[G2_BM * 16],
                                            f32x16v (&acc)[NH][G2_MB / NH], int m0, int ltile,
                                            int b0, int mw, int g0, int g1, int wave,
@@ -332,14 +186,8 @@ __device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
     const int sb = (g - g0) & 1;
     const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
     if (g + 1 < g1) {
-#if !(QW4_G2_DIAG & 1)
       g2_load_act(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave);
-#endif
-#if !(QW4_G2_DIAG & 2)
       g2_load_weights(nxt, rs, a.G, ltile, b0, g + 1, lane);
-#else
-      nxt = cur;
-#endif
     }
     float sf[NH], cf[NH];
 #pragma unroll
@@ -375,7 +223,6 @@ __device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
         for (int j = 0; j < NH; ++j)
           acc[j][mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
               wd[cu][j], __builtin_bit_cast(bf16x8, xo[cu][mb]), acc[j][mb], 0, 0, 0);
-#ifndef QW4_G2_NOSCHED
       if (u + 1 < 8) {
 #pragma unroll
         for (int i = 0; i < MBW * NH; ++i) {
@@ -384,7 +231,6 @@ __device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
           __builtin_amdgcn_sched_group_barrier(0x002, 4 * NH, 0);  // VALU
         }
       }
-#endif
     }
     cur = nxt;
   }
@@ -393,7 +239,7 @@ __device__ __forceinline__ void g2_segment(const Gemm2Args& a, const G2Rsrc& rs,
 // D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
 // columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
 template <int NH>
-__device__ __forceinline__ void g2_store(const Gemm2Args& a, const f32x16v (&acc)[NH][G2_MB / NH],
+__device__ __forceinline__ void g2_store(const GemmArgs& a, const f32x16v (&acc)[NH][G2_MB / NH],
                                          int m0, int tile, int b0, int mw, int lane) {
   constexpr int MBW = G2_MB / NH;
   const int r = lane & 31, h = lane >> 5;
@@ -416,7 +262,7 @@ __device__ __forceinline__ void g2_store(const Gemm2Args& a, const f32x16v (&acc
 // Stream-K partial tiles. Each workgroup has two fp32 slots (for its first
 // and its last tile), laid out [wave][m-block][lane] in 64-byte runs. A
 // workgroup whose range cuts a tile writes its partial there; a second kernel
-// (k_gemm2_fixup, stream-ordered after this one) sums each cut tile's slots in
+// (k_gemm_fixup, stream-ordered after this one) sums each cut tile's slots in
 // workgroup order -- a fixed order, so results are bitwise reproducible -- and
 // stores the tile.
 constexpr uint32_t kSlotBytes = (uint32_t)G2_BM * G2_BN * 4;   // 256 KiB
@@ -446,18 +292,18 @@ __device__ __forceinline__ void g2_slot_store(__amdgpu_buffer_rsrc_t rs,
     }
 }
 
-__device__ __forceinline__ int g2_range_start(const Gemm2Args& a, int vp) {
+__device__ __forceinline__ int g2_range_start(const GemmArgs& a, int vp) {
   return (int)((long long)vp * a.U / a.P);
 }
 // Largest vp with g2_range_start(vp) <= u.
-__device__ __forceinline__ int g2_owner_of(const Gemm2Args& a, int u) {
+__device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
   return (int)(((long long)(u + 1) * a.P - 1) / a.U);
 }
 
 // One workgroup per tile (8 waves, the main kernel's wave -> row mapping);
 // tiles that a single workgroup covered were stored by the main kernel.
 template <int NH>
-__global__ __launch_bounds__(512) void k_gemm2_fixup(Gemm2Args a) {
+__global__ __launch_bounds__(512) void k_gemm_fixup(GemmArgs a) {
   constexpr int MBW = G2_MB / NH;
   const int t = blockIdx.x;
   const int p0 = g2_owner_of(a, t * a.G), p1 = g2_owner_of(a, t * a.G + a.G - 1);
@@ -497,7 +343,7 @@ __global__ __launch_bounds__(512) void k_gemm2_fixup(Gemm2Args a) {
 }
 
 template <int NH>
-__global__ __launch_bounds__(512, 1) void k_gemm2(Gemm2Args a) {
+__global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
   constexpr int MBW = G2_MB / NH;           // m-blocks per wave
   __shared__ u32x4 lds[2][G2_BM * 16];      // 2 x 64 KiB: [row][16 swizzled chunks]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
@@ -592,13 +438,11 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
   if (st) return st;
   if (!C || !A) return QW4_ERR_NULL;
   if (M < 1) return QW4_ERR_M;
-  if (((uintptr_t)A & 15) || ((uintptr_t)C & 1)) return QW4_ERR_ALIGN;
-  static const int version = [] {
-    const char* e = std::getenv("QW4_GEMM_V");
-    return e ? std::atoi(e) : 2;
-  }();
-  if (version == 2) {
-    if (((uintptr_t)C & 7)) return QW4_ERR_ALIGN;
+  if (((uintptr_t)A & 15) || ((uintptr_t)C & 7)) return QW4_ERR_ALIGN;
+  // Loads address A and the weights through 32-bit buffer offsets.
+  if ((size_t)M * w->in_f * 2 >= (1ull << 32) || (size_t)w->out_f * w->in_f / 2 >= (1ull << 32))
+    return QW4_ERR_SHAPE;
+  {
     const int tiles_n = (w->out_f + G2_BN - 1) / G2_BN;
     const int tiles_m = (M + G2_BM - 1) / G2_BM;
     static const int map_env = [] {
@@ -606,7 +450,7 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
       return e ? std::atoi(e) : 1;
     }();
     const int nt = tiles_n * tiles_m;
-    Gemm2Args a{w->qweight, w->scale, w->zeros, A, C, nullptr, M, w->out_f, w->in_f,
+    GemmArgs a{w->qweight, w->scale, w->zeros, A, C, nullptr, M, w->out_f, w->in_f,
                 w->num_groups, tiles_n, tiles_m, map_env && nt % 8 == 0, nt, nt * w->num_groups};
     int grid = nt;
     // Stream-K (one workgroup per CU, the (tile, group) units split evenly)
@@ -636,21 +480,16 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
       return e ? std::atoi(e) : 1;
     }();
     hipStream_t s = (hipStream_t)stream;
-    if (nh == 2) k_gemm2<2><<<grid, 512, 0, s>>>(a);
-    else k_gemm2<1><<<grid, 512, 0, s>>>(a);
+    if (nh == 2) k_gemm<2><<<grid, 512, 0, s>>>(a);
+    else k_gemm<1><<<grid, 512, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
     if (grid != nt) {
-      if (nh == 2) k_gemm2_fixup<2><<<nt, 512, 0, s>>>(a);
-      else k_gemm2_fixup<1><<<nt, 512, 0, s>>>(a);
+      if (nh == 2) k_gemm_fixup<2><<<nt, 512, 0, s>>>(a);
+      else k_gemm_fixup<1><<<nt, 512, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;
   }
-  GemmArgs a{w->qweight, w->scale, w->zeros, A, C, M, w->out_f, w->in_f, w->num_groups};
-  const int grid = ((M + BM - 1) / BM) * ((w->out_f + BN - 1) / BN);
-  k_gemm<<<grid, 256, 0, (hipStream_t)stream>>>(a);
-  QW4_LAUNCH_CHECK();
-  return QW4_OK;
 }
 
 }  // extern "C"

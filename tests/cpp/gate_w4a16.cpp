@@ -109,7 +109,7 @@ int main() {
   uint16_t* d_C = nullptr;
   CK(hipMalloc(&d_C, (size_t)Mp * N * 2));
   qwen::GemmWorkspace ws;
-  qwen::gemm_workspace_alloc(ws, 0);
+  qwen::gemm_workspace_alloc(ws, 256ull << 20);   // as the reference sizes it (model.cu:440)
   qwen::gemm_w4a16(reinterpret_cast<__hip_bfloat16*>(d_C), W,
                    reinterpret_cast<__hip_bfloat16*>(d_A), Mp, ws);
   std::vector<uint16_t> Cm((size_t)Mp * N);
