@@ -98,7 +98,7 @@ int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows,
 typedef struct qw4_scratch {
   float* partial;          /* split-K partials                               */
   uint32_t* counters;      /* per-tile arrival counters (+1 argmax counter)  */
-  uint64_t* keys;          /* argmax keys, one per row                       */
+  uint64_t* keys;          /* argmax keys: 64 groups x 16 rows               */
   size_t partial_elems;
   int32_t max_in, max_out, max_m, max_tiles;
 } qw4_scratch;

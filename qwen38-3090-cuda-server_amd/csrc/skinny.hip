@@ -88,7 +88,6 @@ struct SkinnyArgs {
                         //   [max_tiles, +64)      argmax arrival, per key group
                         //   [max_tiles + 64]      argmax arrival, of key groups
   uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
-  const uint16_t* zero_row;   // >= K bf16 zeros: the activation row of lanes m >= M
   int M, N, K, G, tiles, max_tiles, P, U;
   uint32_t slot_bytes;
 };
@@ -137,19 +136,40 @@ struct GroupData {
   uint32_t z;   // zero points of rows 4c..4c+3 (4 bits each)
 };
 
-// xrow: this lane's activation row (row c of x, or the zero row for c >= M),
-// offset by its k chunk -- a pointer select instead of masking 16 registers.
-__device__ __forceinline__ void load_group(GroupData& d, const SkinnyArgs& a, int b, int g,
-                                           int c, int q, const uint16_t* xrow) {
-  const size_t blk = (size_t)b * a.G + g;
-  const uint32_t* wp = a.qw + blk * kWordsPerBlock + q * 256 + c * 4;
+// Buffer-resource loads: a loop-invariant per-lane offset plus a wave-uniform
+// scalar offset per block. Activation rows past M lie outside the x resource
+// (M rows of K) and read as zeros without touching memory: for M = 1, 60 of
+// the 64 lanes issue no activation traffic.
+struct SkinnyRsrc {
+  __amdgpu_buffer_rsrc_t qw, sc, zr, x;
+};
+
+__device__ __forceinline__ SkinnyRsrc skinny_rsrc(const SkinnyArgs& a) {
+  SkinnyRsrc r;
+  r.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0,
+                                           (int)((uint32_t)a.N * (uint32_t)a.K / 2u), 0x00020000);
+  r.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0,
+                                           (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
+  r.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
+                                           (int)((uint32_t)a.N * (uint32_t)a.G / 2u), 0x00020000);
+  r.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0,
+                                          (int)((uint32_t)a.M * (uint32_t)a.K * 2u), 0x00020000);
+  return r;
+}
+
+// xoff: this lane's byte offset into x (row c, k chunk q; out of range for
+// c >= M). woff: its offset inside a 4 KiB block (chunk q, position c).
+__device__ __forceinline__ void load_group(GroupData& d, const SkinnyRsrc& r, const SkinnyArgs& a,
+                                           int b, int g, int c, uint32_t woff, uint32_t xoff) {
+  const uint32_t blk = (uint32_t)b * (uint32_t)a.G + (uint32_t)g;
 #pragma unroll
-  for (int st = 0; st < 4; ++st) d.w[st] = *reinterpret_cast<const u32x4*>(wp + st * 64);
-  const uint16_t* xp = xrow + (size_t)g * kGroup;
+  for (int st = 0; st < 4; ++st)
+    d.w[st] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + st * 256, blk * 4096u, 0);
 #pragma unroll
-  for (int t = 0; t < 4; ++t) d.x[t] = *reinterpret_cast<const u32x4*>(xp + 8 * t);
-  d.s = *reinterpret_cast<const u32x2*>(a.sc + blk * 64 + 4 * c);
-  d.z = a.zr[blk * 16 + c];
+  for (int t = 0; t < 4; ++t)
+    d.x[t] = __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
+  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * 128u, 0);
+  d.z = __builtin_amdgcn_raw_buffer_load_b16(r.zr, (uint32_t)c * 2u, blk * 32u, 0);
 }
 
 __device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, NibConst k) {
@@ -389,7 +409,9 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   __shared__ f32x4 stash[4][64];   // M = 1: the first split tile's sums
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
-  const uint16_t* xrow = (c < a.M ? a.x + (size_t)c * a.K : a.zero_row) + 32 * q;
+  const SkinnyRsrc rs = skinny_rsrc(a);
+  const uint32_t woff = (uint32_t)(q * 1024 + c * 16);
+  const uint32_t xoff = (uint32_t)(c * a.K + 32 * q) * 2u;
   const int p = blockIdx.x;
   const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
   if (u0 >= u1) return;   // whole workgroup: no work
@@ -412,8 +434,8 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
     for (int g = lo + wave; g < hi; g += kBatch * W) {
       GroupData d0, d1;
       const bool two = kBatch == 2 && g + W < hi;
-      load_group(d0, a, sb, g, c, q, xrow);
-      if (two) load_group(d1, a, sb, g + W, c, q, xrow);
+      load_group(d0, rs, a, sb, g, c, woff, xoff);
+      if (two) load_group(d1, rs, a, sb, g + W, c, woff, xoff);
       mma_group(acc, d0, k);
       if (two) mma_group(acc, d1, k);
     }
@@ -546,6 +568,11 @@ Launch launch_for(int out_f, int G) {
   else
     cap = (long long)tiles * (l.W == 16 ? 2 : 1);
   if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
+  static const int env_p = [] {
+    const char* e = std::getenv("QW4_SKINNY_P");
+    return e ? std::atoi(e) : 0;
+  }();
+  if (env_p > 0) cap = env_p;
   // at most 64 workgroups may share a tile: keep ranges >= G / 60 blocks
   cap = std::min(cap, std::max<long long>(1, U * 60 / G));
   l.P = (int)std::max<long long>(1, std::min(cap, (U + l.W - 1) / l.W));
@@ -577,6 +604,8 @@ int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scra
     return QW4_ERR_ALIGN;
   const int tiles = w->out_f / kTileN;
   if (tiles > s->max_tiles || M > s->max_m || w->in_f > s->max_in) return QW4_ERR_SCRATCH;
+  // loads address weights and x through 32-bit buffer offsets
+  if ((size_t)w->out_f * w->in_f / 2 >= (1ull << 32)) return QW4_ERR_SHAPE;
   const bool m1 = M == 1;
   const Launch l = m1 ? launch_for<OUT, true>(w->out_f, w->num_groups)
                       : launch_for<OUT, false>(w->out_f, w->num_groups);
@@ -593,7 +622,6 @@ int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scra
   a.sums = reinterpret_cast<uint64_t*>(s->partial + slot_floats());
   a.counters = s->counters;
   a.keys = s->keys;
-  a.zero_row = reinterpret_cast<const uint16_t*>(s->keys + kKeyGroups * 16);
   a.M = M;
   a.N = w->out_f;
   a.K = w->in_f;
@@ -640,8 +668,8 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
   // slots (M > 1) for the largest grid, then one fixed-point word per column
   s->partial_elems = slot_floats() + (size_t)s->max_tiles * 64 * 2;
   const size_t cnt_bytes = (size_t)(s->max_tiles + kKeyGroups + 1) * kCounterStride * 4;
-  // argmax keys, then a zero activation row of max_in bf16 (never written)
-  const size_t key_bytes = (size_t)kKeyGroups * 16 * 8 + (size_t)max_in * 2 + 256;
+  // argmax keys: one 128-byte line per key group
+  const size_t key_bytes = (size_t)kKeyGroups * 16 * 8;
   hipError_t e = hipMalloc((void**)&s->partial, s->partial_elems * 4);
   if (e == hipSuccess) e = hipMemset(s->partial, 0, s->partial_elems * 4);
   if (e == hipSuccess) e = hipMalloc((void**)&s->counters, cnt_bytes);
