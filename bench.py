@@ -276,6 +276,36 @@ class Bench:
         self.extra["config3_verify"] = c3
         log(f"config3: {c3}")
 
+        # One GPU's share of an 8-way tensor-parallel layer (qkv and gate|up split
+        # by rows, o and down by columns; the all-reduce after o/down is not
+        # part of this kernel): the same 64-layer sweep at shard shapes.
+        shard = (("qkv", 5120, 896), ("o_proj", 512, 5120), ("gate|up", 5120, 4352),
+                 ("down", 2176, 5120))
+        sw = [[self.weights(N, K, 20000 + 8 * l + t) for t, (_, K, N) in enumerate(shard)]
+              for l in range(len(self.layers))]
+
+        def shard_step():
+            for lw in sw:
+                for (_, K, N), w in zip(shard, lw):
+                    hip.gemv_w4a16(ys, w, xs[K] if K in xs else self.xs_shard[K], scratch)
+
+        self.xs_shard = {}
+        for K in (512, 2176):
+            x = torch.empty((16, K), dtype=torch.int16, device="cuda")
+            hip.gen_bf16(x, 16 * K, 0, 1000 + K, 0)
+            self.xs_shard[K] = x
+        g_sh = self.capture(shard_step)
+        t_sh = self.time_graph(g_sh, 5)
+        del g_sh
+        b_sh = sum(alg_bytes(1, K, N) for _, K, N in shard) * len(sw)
+        self.extra["config2_shard8"] = {
+            "shapes": "qkv 5120->896, o 512->5120, gate|up 5120->4352, down 2176->5120",
+            "ms_per_sweep": round(t_sh, 3), "GBps": round(b_sh / (t_sh * 1e-3) / 1e9, 1)}
+        for lw in sw:
+            for w in lw:
+                hip.awq_free(w)
+        log(f"config2 shard8: {self.extra['config2_shard8']}")
+
         wl = self.weights(248320, 5120, 9500)
         idx = torch.empty(16, dtype=torch.int32, device="cuda")
         c5 = {}

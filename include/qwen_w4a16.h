@@ -14,7 +14,7 @@
  * reference callers keep their behaviour.
  *
  * Weight format accepted: INT4, asymmetric, group 128, stored nibbles 0..15
- * (w = (q - zp) * scale). Shapes: out_f % 64 == 0, in_f % 512 == 0.
+ * (w = (q - zp) * scale). Shapes: out_f % 64 == 0, in_f % 128 == 0.
  */
 #ifndef QWEN_W4A16_H
 #define QWEN_W4A16_H
@@ -30,7 +30,7 @@ extern "C" {
 enum {
   QW4_OK = 0,
   QW4_ERR_NULL = 1,        /* a required pointer is NULL                         */
-  QW4_ERR_SHAPE = 2,       /* out_f % 64, in_f % 512, row offset or M invalid    */
+  QW4_ERR_SHAPE = 2,       /* out_f % 64, in_f % 128, row offset or M invalid    */
   QW4_ERR_GROUP = 3,       /* group_size other than 128                          */
   QW4_ERR_M = 4,           /* M outside the range the entry point supports       */
   QW4_ERR_SCRATCH = 5,     /* scratch / workspace too small for this call        */

@@ -19,7 +19,7 @@
 //   * GemmWorkspace holds no BLAS handle and no dequantized weights: the prefill
 //     GEMM is one fused kernel; a workspace of >= 2 x CUs x 256 KiB lets it
 //     split tiles across workgroups (stream-K partials live there).
-//   * group_size must be 128; out_f % 64 == 0 and in_f % 512 == 0.
+//   * group_size must be 128; out_f % 64 == 0 and in_f % 128 == 0.
 #pragma once
 #include <hip/hip_bf16.h>
 #include <hip/hip_runtime.h>

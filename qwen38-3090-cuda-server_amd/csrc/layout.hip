@@ -218,7 +218,7 @@ __global__ __launch_bounds__(256) void k_stream_read(const u32x4* __restrict__ s
 int check_weights(const qw4_weights* w) {
   if (!w || !w->qweight || !w->scale || !w->zeros) return QW4_ERR_NULL;
   if (w->group_size != kGroup) return QW4_ERR_GROUP;
-  if (w->out_f <= 0 || w->out_f % kTileN || w->in_f <= 0 || w->in_f % 512 ||
+  if (w->out_f <= 0 || w->out_f % kTileN || w->in_f <= 0 || w->in_f % kGroup ||
       w->num_groups != w->in_f / kGroup)
     return QW4_ERR_SHAPE;
   return QW4_OK;
@@ -240,7 +240,7 @@ const char* qw4_status_string(int st) {
   switch (st) {
     case QW4_OK: return "ok";
     case QW4_ERR_NULL: return "null pointer";
-    case QW4_ERR_SHAPE: return "unsupported shape (out_f % 64, in_f % 512, row offset or size)";
+    case QW4_ERR_SHAPE: return "unsupported shape (out_f % 64, in_f % 128, row offset or size)";
     case QW4_ERR_GROUP: return "unsupported group size (only 128)";
     case QW4_ERR_M: return "M out of range for this entry point";
     case QW4_ERR_SCRATCH: return "scratch or workspace too small";
@@ -265,7 +265,7 @@ int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void*
   (void)stream;
   if (!w) return QW4_ERR_NULL;
   if (group_size != kGroup) return QW4_ERR_GROUP;
-  if (out_f <= 0 || out_f % kTileN || in_f <= 0 || in_f % 512) return QW4_ERR_SHAPE;
+  if (out_f <= 0 || out_f % kTileN || in_f <= 0 || in_f % kGroup) return QW4_ERR_SHAPE;
   std::memset(w, 0, sizeof(*w));
   w->out_f = out_f;
   w->in_f = in_f;

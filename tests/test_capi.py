@@ -69,7 +69,12 @@ def test_argument_errors_before_any_launch(hip):
     assert L.qw4_gemv(y, C.byref(wg), x, C.byref(s), None) == hip.QW4_ERR_GROUP
     # shapes the layout cannot hold
     assert L.qw4_gemv(y, C.byref(_fake_weights(hip, out_f=96)), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
-    assert L.qw4_gemv(y, C.byref(_fake_weights(hip, in_f=640)), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    bad_k = _fake_weights(hip, in_f=640)
+    bad_k.in_f = 600                       # not a whole number of 128-wide groups
+    assert L.qw4_gemv(y, C.byref(bad_k), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    bad_g = _fake_weights(hip, in_f=640)
+    bad_g.num_groups = 4                   # inconsistent with in_f
+    assert L.qw4_gemv(y, C.byref(bad_g), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
     # scratch too small for the output rows / M (reference: gemv_partial_check aborts)
     small = _fake_scratch(hip, max_m=4, tiles=1)
     assert L.qw4_gemv(y, C.byref(w), x, C.byref(small), None) == hip.QW4_ERR_SCRATCH

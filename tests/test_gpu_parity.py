@@ -65,7 +65,7 @@ def test_generator_matches_oracle(hip, orc):
 
 
 # ------------------------------------------------------------ repack/dequant
-@pytest.mark.parametrize("N,K", [(64, 512), (192, 1024), (320, 5120)])
+@pytest.mark.parametrize("N,K", [(64, 512), (192, 1024), (320, 5120), (128, 384), (64, 2176)])
 def test_repack_layouts_agree_and_dequant_bitexact(hip, orc, N, K):
     import torch
 
@@ -157,7 +157,11 @@ def test_gemv_config1(hip, orc, scratch):
 
 
 @pytest.mark.parametrize("N,K", [(64, 512), (64, 4096), (7168, 5120), (5120, 4096),
-                                 (5120, 17408), (34816, 5120)])
+                                 (5120, 17408), (34816, 5120),
+                                 # one GPU's shard of an 8-way split: qkv and gate|up by
+                                 # rows (N / 8), o and down by columns (K / 8), lm_head
+                                 (896, 5120), (4352, 5120), (5120, 512), (5120, 2176),
+                                 (31040, 5120), (64, 640)])
 def test_gemv_layer_shapes(hip, orc, scratch, N, K):
     w, _, y, ref = _run_gemv(hip, orc, scratch, N, K, seed=N + K)
     _check_bf16(orc, host(y, np.uint16), ref, f"gemv {N}x{K}")
@@ -165,7 +169,7 @@ def test_gemv_layer_shapes(hip, orc, scratch, N, K):
 
 
 @pytest.mark.parametrize("M", [2, 9, 12, 16])
-@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 17408), (128, 1024)])
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 17408), (128, 1024), (5120, 2176)])
 def test_verify_skinny(hip, orc, scratch, M, N, K):
     """speculative-verify M in {9, 12, 16} (and M=2)."""
     w, _, y, ref = _run_gemv(hip, orc, scratch, N, K, seed=3 * M + N, M=M)
@@ -237,7 +241,8 @@ def gemm_ws(hip):
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 512), (77, 320, 1024), (512, 17408, 5120),
-                                   (512, 5120, 17408), (200, 5184, 1536), (777, 5184, 4096)])
+                                   (512, 5120, 17408), (200, 5184, 1536), (777, 5184, 4096),
+                                   (300, 5120, 2176), (64, 896, 640)])
 @pytest.mark.parametrize("use_ws", [False, True])
 def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     """BASELINE config 4 semantics: RNE(bf16) dequant, fp32 accumulation, bf16 out.
