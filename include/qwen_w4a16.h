@@ -37,7 +37,9 @@ enum {
   QW4_ERR_ALIGN = 6,       /* activation / output pointer not 16-byte aligned    */
   QW4_ERR_HIP = 7,         /* a HIP runtime call failed (see qw4_last_hip_error)  */
   QW4_ERR_NOMEM = 8,       /* device allocation failed                           */
-  QW4_ERR_LAYOUT = 9       /* unknown source layout id                           */
+  QW4_ERR_LAYOUT = 9,      /* unknown source layout id                           */
+  QW4_ERR_IO = 10,         /* file cannot be opened, mapped or parsed            */
+  QW4_ERR_NOTFOUND = 11    /* tensor absent from a safetensors file              */
 };
 
 const char* qw4_status_string(int status);
@@ -167,6 +169,38 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M,
  * >= 512 int32 (the reference's 256 (idx, val) pairs). */
 int qw4_argmax(int32_t* out, const uint16_t* x, int n, int32_t* scratch, void* stream);
 int qw4_argmax_rows(int32_t* out, const uint16_t* x, int rows, int n, void* stream);
+
+/* ---------------------------------------------------------- checkpoints
+ * mmap'd safetensors reader (src/loader/safetensors.h:44-75; C++ API in
+ * qwen_safetensors.hpp) and the compressed-tensors -> repacked loader.
+ * Host code only: a qw4_st_tensor's data points into the read-only mapping and
+ * stays valid until qw4_st_close. dtype uses the safetensors dtype order
+ * BF16, F16, F32, F64, I8, U8, I16, I32, I64, BOOL, F8_E4M3, F8_E5M2 = 0..11. */
+typedef struct qw4_st qw4_st;
+typedef struct qw4_st_tensor {
+  int32_t dtype;
+  int32_t ndim;            /* dims beyond 8 are not reported */
+  int64_t shape[8];
+  const void* data;
+  size_t nbytes;
+} qw4_st_tensor;
+
+/* SafeTensors::open_files / open_dir (safetensors.h:53-55). */
+int qw4_st_open(qw4_st** st, const char* const* paths, int npaths);
+int qw4_st_open_dir(qw4_st** st, const char* dir);
+int qw4_st_close(qw4_st* st);
+int qw4_st_count(const qw4_st* st);
+/* SafeTensors::find (safetensors.h:60); QW4_ERR_NOTFOUND if absent. */
+int qw4_st_find(const qw4_st* st, const char* name, qw4_st_tensor* out);
+/* Message of the last QW4_ERR_IO / _NOTFOUND / _SHAPE from these calls (this thread). */
+const char* qw4_st_last_error(void);
+/* fuse() (src/model/model.cu:103-128): allocate w for the sum of the parts'
+ * rows and repack each part's <prefix>.weight_packed (I32 [rows][in_f/8]),
+ * .weight_scale (BF16 [rows][G]) and .weight_zero_point (I32 [rows/8][G]) at
+ * consecutive row offsets (each part's rows % 64 == 0). Synchronizes the
+ * stream (the uploaded sources are freed before returning). */
+int qw4_load_ct_fused(qw4_weights* w, const qw4_st* st, const char* const* prefixes,
+                      int nparts, int in_f, int group_size, void* stream);
 
 /* ------------------------------------------------- synthetic inputs
  * Device-side generator for the benchmark (no reference counterpart). The

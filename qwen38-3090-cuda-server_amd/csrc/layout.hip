@@ -248,6 +248,8 @@ const char* qw4_status_string(int st) {
     case QW4_ERR_HIP: return "HIP runtime error";
     case QW4_ERR_NOMEM: return "device allocation failed";
     case QW4_ERR_LAYOUT: return "unknown source layout";
+    case QW4_ERR_IO: return "checkpoint file cannot be opened, mapped or parsed";
+    case QW4_ERR_NOTFOUND: return "tensor not found in the checkpoint";
     default: return "unknown status";
   }
 }

@@ -27,6 +27,8 @@ QW4_ERR_ALIGN = 6
 QW4_ERR_HIP = 7
 QW4_ERR_NOMEM = 8
 QW4_ERR_LAYOUT = 9
+QW4_ERR_IO = 10
+QW4_ERR_NOTFOUND = 11
 LAYOUT_AWQ_K = 1
 LAYOUT_AWQ_N = 2
 
@@ -38,14 +40,24 @@ EXPORTS = (
     "qw4_partial_check", "qw4_choose_splits", "qw4_gemv", "qw4_gemv_f32", "qw4_gemm_small",
     "qw4_gemm_mma", "qw4_gemv_argmax", "qw4_workspace_alloc", "qw4_workspace_free",
     "qw4_gemm", "qw4_argmax", "qw4_argmax_rows", "qw4_gen_bf16", "qw4_gen_awq_k",
-    "qw4_stream_read",
+    "qw4_stream_read", "qw4_st_open", "qw4_st_open_dir", "qw4_st_close", "qw4_st_count",
+    "qw4_st_find", "qw4_st_last_error", "qw4_load_ct_fused",
 )
+
+# safetensors dtype order (qw4_st_tensor.dtype)
+ST_DTYPES = ("BF16", "F16", "F32", "F64", "I8", "U8", "I16", "I32", "I64", "BOOL", "F8_E4M3",
+             "F8_E5M2")
 
 
 class W4A16Error(RuntimeError):
     def __init__(self, status: int, where: str):
         self.status = status
         msg = lib().qw4_status_string(status).decode()
+        if status in (QW4_ERR_IO, QW4_ERR_NOTFOUND) or (
+                status == QW4_ERR_SHAPE and where.startswith(("load_ct_fused", "SafeTensors"))):
+            detail = lib().qw4_st_last_error().decode()
+            if detail:
+                msg += f": {detail}"
         if status == QW4_ERR_HIP:
             msg += f" (hipError {lib().qw4_last_hip_error()})"
         super().__init__(f"{where}: {msg} [status {status}]")
@@ -71,6 +83,12 @@ class GemvScratch(C.Structure):
 class GemmWorkspace(C.Structure):
     """qw4_workspace / the reference's GemmWorkspace (gemm_w4a16.cuh:30-35)."""
     _fields_ = [("buf", C.c_void_p), ("bytes", C.c_size_t)]
+
+
+class StTensor(C.Structure):
+    """qw4_st_tensor: one tensor of an open safetensors set (host view)."""
+    _fields_ = [("dtype", C.c_int32), ("ndim", C.c_int32), ("shape", C.c_int64 * 8),
+                ("data", C.c_void_p), ("nbytes", C.c_size_t)]
 
 
 _lib = None
@@ -114,6 +132,13 @@ def lib():
         "qw4_gen_bf16": ([vp, sz, u64, u64, u64, i, vp], i),
         "qw4_gen_awq_k": ([vp, vp, vp, i, i, u64, u64, vp], i),
         "qw4_stream_read": ([vp, sz, vp, i, vp], i),
+        "qw4_st_open": ([C.POINTER(vp), C.POINTER(C.c_char_p), i], i),
+        "qw4_st_open_dir": ([C.POINTER(vp), C.c_char_p], i),
+        "qw4_st_close": ([vp], i),
+        "qw4_st_count": ([vp], i),
+        "qw4_st_find": ([vp, C.c_char_p, C.POINTER(StTensor)], i),
+        "qw4_st_last_error": ([], C.c_char_p),
+        "qw4_load_ct_fused": ([W, vp, C.POINTER(C.c_char_p), i, i, i, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -326,3 +351,65 @@ def stream_read(src, nbytes: int, sink, blocks: int, stream=None) -> None:
     _need(sink, blocks * 4, "stream_read sink")
     _chk(lib().qw4_stream_read(_ptr(src), nbytes, _ptr(sink), blocks, _stream(stream)),
          "stream_read")
+
+
+# ------------------------------------------------------------ checkpoints
+class SafeTensors:
+    """The reference's qwen::SafeTensors (src/loader/safetensors.h:44-75) over
+    the C-ABI: files are mmap'd by the library; get() returns a numpy view of
+    the mapping (valid until close())."""
+
+    def __init__(self, paths=None, dir=None):
+        self._h = C.c_void_p()
+        if dir is not None:
+            _chk(lib().qw4_st_open_dir(C.byref(self._h), dir.encode()), "SafeTensors.open_dir")
+        else:
+            arr = (C.c_char_p * len(paths))(*[p.encode() for p in paths])
+            _chk(lib().qw4_st_open(C.byref(self._h), arr, len(paths)), "SafeTensors.open_files")
+
+    def close(self) -> None:
+        if self._h:
+            lib().qw4_st_close(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __len__(self) -> int:
+        return lib().qw4_st_count(self._h)
+
+    def info(self, name: str) -> StTensor:
+        t = StTensor()
+        _chk(lib().qw4_st_find(self._h, name.encode(), C.byref(t)), f"SafeTensors.find({name})")
+        return t
+
+    def has(self, name: str) -> bool:
+        t = StTensor()
+        return lib().qw4_st_find(self._h, name.encode(), C.byref(t)) == QW4_OK
+
+    def get(self, name: str):
+        import numpy as np
+
+        t = self.info(name)
+        np_dt = {"BF16": np.uint16, "F16": np.float16, "F32": np.float32, "F64": np.float64,
+                 "I8": np.int8, "U8": np.uint8, "I16": np.int16, "I32": np.int32,
+                 "I64": np.int64, "BOOL": np.bool_, "F8_E4M3": np.uint8,
+                 "F8_E5M2": np.uint8}[ST_DTYPES[t.dtype]]
+        shape = tuple(t.shape[k] for k in range(t.ndim))
+        buf = (C.c_uint8 * t.nbytes).from_address(t.data) if t.nbytes else b""
+        return np.frombuffer(buf, dtype=np_dt).reshape(shape)
+
+    def dtype(self, name: str) -> str:
+        return ST_DTYPES[self.info(name).dtype]
+
+    def load_ct_fused(self, prefixes, in_f: int, group_size: int = 128, stream=None) -> W4A16Weights:
+        """fuse() (src/model/model.cu:103-128): repack the compressed-tensors
+        projections `prefixes` into one W4A16 tensor, rows in order."""
+        w = W4A16Weights()
+        arr = (C.c_char_p * len(prefixes))(*[p.encode() for p in prefixes])
+        _chk(lib().qw4_load_ct_fused(C.byref(w), self._h, arr, len(prefixes), in_f, group_size,
+                                     _stream(stream)), "load_ct_fused")
+        return w

@@ -301,6 +301,49 @@ def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
     hip.awq_free(w)
 
 
+# ------------------------------------------------------------ checkpoints
+def test_checkpoint_fused_load(hip, orc, scratch, tmp_path):
+    """SURVEY next-row 1: a compressed-tensors checkpoint (weight_packed I32
+    [N][K/8], weight_scale BF16 [N][G], weight_zero_point I32 [N/8][G], the
+    reference's on-disk format) read by the library's safetensors reader and
+    fused like the reference's fuse() (model.cu:103-128): q, k and v of one
+    layer into one tensor. The dequantized rows are bit-exact against the
+    oracle and the GEMV matches it."""
+    import torch
+    from safetensors.torch import save_file
+
+    K = 1024
+    parts = (("model.layers.3.self_attn.q_proj", 256), ("model.layers.3.self_attn.k_proj", 64),
+             ("model.layers.3.self_attn.v_proj", 128))
+    logical, tensors = [], {}
+    for t, (name, n) in enumerate(parts):
+        q, zp, s = orc.gen_weights(n, K, seed=31, tensor=t)
+        p, sc, z = orc.pack_ct(q, zp, s)
+        tensors[name + ".weight_packed"] = torch.from_numpy(p.view(np.int32).copy())
+        tensors[name + ".weight_scale"] = torch.from_numpy(sc.view(np.int16).copy()).view(
+            torch.bfloat16)
+        tensors[name + ".weight_zero_point"] = torch.from_numpy(z.view(np.int32).copy())
+        logical.append((q, zp, s))
+    path = str(tmp_path / "model-00001-of-00001.safetensors")
+    save_file(tensors, path)
+    st = hip.SafeTensors(paths=[path])
+    w = st.load_ct_fused([name for name, _ in parts], in_f=K)
+    st.close()
+    N = sum(n for _, n in parts)
+    assert (w.out_f, w.in_f, w.num_groups) == (N, K, K // 128)
+    q = np.concatenate([l[0] for l in logical]); zp = np.concatenate([l[1] for l in logical])
+    s = np.concatenate([l[2] for l in logical])
+    deq = empty((N, K), np.uint16)
+    hip.w4a16_dequant_rows(deq, w, 0, N)
+    x = orc.gen_x(1, K, seed=5)
+    y = empty((1, N), np.uint16)
+    hip.gemv_w4a16(y, w, dev(x), scratch)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(deq, np.uint16), orc.dequant_bf16(q, zp, s))
+    _check_bf16(orc, host(y, np.uint16), orc.matmul_f64(x, q, zp, s), "checkpoint qkv")
+    hip.awq_free(w)
+
+
 # ------------------------------------------------------------ bf16 argmax
 def test_argmax_bf16_entry_points(hip, orc):
     import torch
