@@ -321,6 +321,24 @@ class Bench:
         hip.awq_free(wl)
         log(f"config5: {c5}")
 
+        # The reference's default head format: 8-bit weights (lm_head_bits 8).
+        src = torch.empty(248320 * 5120, dtype=torch.int16, device="cuda")
+        hip.gen_bf16(src, src.numel(), 0, 9600, 0)
+        w8 = hip.quantize_w8a16(src, 248320, 5120)
+        del src
+        c5w8 = {}
+        b8 = 248320 * 5120 + 248320 * 40 * 2
+        for M in (1, 9):
+            g5 = self.capture(lambda: [hip.gemv_argmax_w8a16(idx, w8, xs[5120], M, scratch)
+                                       for _ in range(10)])
+            us = self.time_graph(g5, 3) / 10 * 1e3
+            del g5
+            c5w8[f"M{M}"] = {"us_per_call": round(us, 2),
+                             "GBps": round((b8 + M * 5120 * 2) / (us * 1e-6) / 1e9, 1)}
+        self.extra["config5_lm_head_w8_argmax"] = c5w8
+        hip.w8a16_free(w8)
+        log(f"config5 w8: {c5w8}")
+
     # ---------------------------------------------------------- config 4
     def prefill(self):
         hip, torch = self.hip, self.torch

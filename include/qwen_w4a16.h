@@ -170,6 +170,42 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M,
 int qw4_argmax(int32_t* out, const uint16_t* x, int n, int32_t* scratch, void* stream);
 int qw4_argmax_rows(int32_t* out, const uint16_t* x, int rows, int n, void* stream);
 
+/* ------------------------------------------------------ 8-bit weights
+ * W8A16Weights (src/kernels/gemv_w4a16.cuh:141-154), the reference's default
+ * lm_head format: per (row, 128-group) a bf16 scale and int8 q in [-127, 127].
+ * Private device layout: 64-row tiles x 128-k groups, 8 KiB blocks, q stored
+ * as q + 128. qweight (out_f * in_f bytes) and scale (out_f * G * 2 bytes) are
+ * separate hipMalloc allocations. */
+typedef struct qw4_w8_weights {
+  uint8_t* qweight;
+  uint16_t* scale;
+  int32_t out_f, in_f, group_size, num_groups;
+} qw4_w8_weights;
+
+/* quantize_w8a16 (gemv_w4a16.cuh:156-157; .cu:478-495, :616-623): allocates w
+ * and quantizes the bf16 source src [out_f][in_f] (16-byte aligned) on the
+ * stream: s = bf16(max|w| / 127), q = clamp(rint(w * 127 / max|w|), +-127). */
+int qw4_w8_quantize(qw4_w8_weights* w, const uint16_t* src, int out_f, int in_f,
+                    int group_size, void* stream);
+/* w8a16_free (gemv_w4a16.cuh:164). */
+int qw4_w8_free(qw4_w8_weights* w);
+size_t qw4_w8_bytes(const qw4_w8_weights* w);   /* W8A16Weights::total_bytes */
+/* dst [nrows][in_f] bf16 = RNE(q * s); no reference counterpart (the 8-bit
+ * analogue of w4a16_dequant_rows, for bit-exact checks). */
+int qw4_w8_dequant_rows(uint16_t* dst, const qw4_w8_weights* w, int row0, int nrows,
+                        void* stream);
+/* gemv_w8a16 (gemv_w4a16.cuh:158-159; .cu:624-636), M = 1, and
+ * gemm_small_w8a16 (gemv_w4a16.cuh:163-164; .cu:551-614), 1 <= M <= 16:
+ * y [M][out_f] bf16, the same kernel as qw4_gemv / qw4_gemm_small. */
+int qw4_w8_gemv(uint16_t* y, const qw4_w8_weights* w, const uint16_t* x, qw4_scratch* s,
+                void* stream);
+int qw4_w8_gemm_small(uint16_t* y, const qw4_w8_weights* w, const uint16_t* x, int M,
+                      qw4_scratch* s, void* stream);
+/* The 8-bit lm_head fused with the fp32 row-argmax: head() with lm_head_bits 8
+ * (src/model/model.cu:796-815, :1044-1047) without writing logits. */
+int qw4_w8_gemv_argmax(int32_t* idx, const qw4_w8_weights* w, const uint16_t* x, int M,
+                       qw4_scratch* s, void* stream);
+
 /* ---------------------------------------------------------- checkpoints
  * mmap'd safetensors reader (src/loader/safetensors.h:44-75; C++ API in
  * qwen_safetensors.hpp) and the compressed-tensors -> repacked loader.

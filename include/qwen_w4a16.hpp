@@ -5,6 +5,7 @@
 // substitutions __nv_bfloat16 -> __hip_bfloat16 (bit-identical) and
 // cudaStream_t -> hipStream_t:
 //   src/kernels/gemv_w4a16.cuh:50-135, :187-188   (W4A16 GEMV / skinny / MMA)
+//   src/kernels/gemv_w4a16.cuh:147-166             (W8A16 lm_head)
 //   src/kernels/gemm_w4a16.cuh:30-48              (prefill GEMM, dequant rows)
 //   src/kernels/elementwise.cuh:39-43              (argmax, argmax_rows)
 // Like the reference, these print a message and abort() on invalid input; the
@@ -83,6 +84,32 @@ void gemm_mma_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat
 // lm_head GEMV + fused fp32 row-argmax (head() + argmax, model.cu:796-815).
 void gemv_argmax_w4a16(int32_t* idx, const W4A16Weights& w, const __hip_bfloat16* x, int M,
                        GemvScratch& s, hipStream_t stream = 0);
+
+// W8A16Weights (gemv_w4a16.cuh:147-154): 8-bit lm_head weights. The device
+// layout is private (64-row tiles, q + 128 bytes); qweight and scale are two
+// separate hipMalloc allocations; total_bytes() keeps the reference's formula.
+struct W8A16Weights {
+  int8_t* qweight = nullptr;
+  __hip_bfloat16* scale = nullptr;
+  int out_f = 0, in_f = 0, group_size = 0, num_groups = 0;
+  size_t total_bytes() const {
+    return size_t(out_f) * in_f + size_t(out_f) * num_groups * 2;
+  }
+};
+
+void quantize_w8a16(W8A16Weights& dst, const __hip_bfloat16* src, int out_f, int in_f,
+                    int group_size, hipStream_t stream = 0);
+void gemv_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,
+                GemvScratch& s, hipStream_t stream = 0);
+void gemm_small_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,
+                      int M, GemvScratch& s, hipStream_t stream = 0);
+void w8a16_free(W8A16Weights& w);
+// 8-bit lm_head + fused fp32 row-argmax (head() with lm_head_bits 8,
+// model.cu:796-815); no reference counterpart as one call.
+void gemv_argmax_w8a16(int32_t* idx, const W8A16Weights& w, const __hip_bfloat16* x, int M,
+                       GemvScratch& s, hipStream_t stream = 0);
+void w8a16_dequant_rows(__hip_bfloat16* dst, const W8A16Weights& w, int row0, int nrows,
+                        hipStream_t stream = 0);
 
 struct GemmWorkspace {
   __hip_bfloat16* wbuf = nullptr;

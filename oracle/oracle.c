@@ -311,6 +311,57 @@ void or_matmul_bf16w_f64(const uint16_t* x, int M, const uint8_t* q, const uint8
   parallel_for(N, nthreads, mm_rows, &c);
 }
 
+/* ------------------------------------------------------------------ W8A16 */
+/* src/kernels/gemv_w4a16.cu:478-495 (k_quant_w8). */
+void or_w8_quantize(const uint16_t* w, int N, int K, int group, int8_t* q, uint16_t* s) {
+  const int G = K / group;
+  for (int n = 0; n < N; ++n)
+    for (int g = 0; g < G; ++g) {
+      const uint16_t* src = w + (size_t)n * K + (size_t)g * group;
+      float mx = 0.f;
+      for (int i = 0; i < group; ++i) mx = fmaxf(mx, fabsf(or_bf16_to_f32(src[i])));
+      const float sc = mx / 127.0f;
+      const float inv = mx > 0.f ? 127.0f / mx : 0.f;
+      s[(size_t)n * G + g] = or_f32_to_bf16(sc);
+      for (int i = 0; i < group; ++i) {
+        const float prod = or_bf16_to_f32(src[i]) * inv;
+        int v = (int)rintf(prod);
+        v = v < -127 ? -127 : (v > 127 ? 127 : v);
+        q[(size_t)n * K + (size_t)g * group + i] = (int8_t)v;
+      }
+    }
+}
+
+typedef struct {
+  const uint16_t* x;
+  int M;
+  const int8_t* q;
+  const uint16_t* s;
+  int N, K, group;
+  double* y;
+} mm8_ctx;
+
+static void mm8_rows(void* p, int lo, int hi) {
+  const mm8_ctx* c = (const mm8_ctx*)p;
+  const int G = c->K / c->group;
+  for (int n = lo; n < hi; ++n)
+    for (int m = 0; m < c->M; ++m) {
+      const uint16_t* xr = c->x + (size_t)m * c->K;
+      double acc = 0.0;
+      for (int k = 0; k < c->K; ++k)
+        acc += (double)c->q[(size_t)n * c->K + k] *
+               (double)or_bf16_to_f32(c->s[(size_t)n * G + k / c->group]) *
+               (double)or_bf16_to_f32(xr[k]);
+      c->y[(size_t)m * c->N + n] = acc;
+    }
+}
+
+void or_w8_matmul_f64(const uint16_t* x, int M, const int8_t* q, const uint16_t* s, int N,
+                      int K, int group, double* y, int nthreads) {
+  mm8_ctx c = {x, M, q, s, N, K, group, y};
+  parallel_for(N, nthreads, mm8_rows, &c);
+}
+
 /* ------------------------------------------------------------ CPU baseline */
 typedef struct {
   const uint16_t* x;

@@ -100,6 +100,17 @@ int or_cpu_w4a16_matmul(const uint16_t* x, int M, const uint32_t* packed,
                         const uint16_t* scale, const uint32_t* zpw, int N, int K,
                         int group, uint16_t* y, int nthreads);
 
+/* ---- W8A16 (the reference's lm_head format, src/kernels/gemv_w4a16.cuh:141-166).
+ * Quantizer, k_quant_w8 (src/kernels/gemv_w4a16.cu:478-495): for each (row n,
+ * group g) of the bf16 source w[N][K], mx = max |w|, s = bf16(mx / 127),
+ * inv = mx > 0 ? 127 / mx : 0 (fp32, from mx, not from the rounded s),
+ * q = clamp(rint(w * inv), -127, 127). Dequantized weight: q * float(s). */
+void or_w8_quantize(const uint16_t* w, int N, int K, int group, int8_t* q, uint16_t* s);
+/* y[m][n] = sum_k x[m][k] * q[n][k] * s[n][k / group], fp64 (k_gemv8,
+ * src/kernels/gemv_w4a16.cu:498-523, with fp64 accumulation). */
+void or_w8_matmul_f64(const uint16_t* x, int M, const int8_t* q, const uint16_t* s, int N,
+                      int K, int group, double* y, int nthreads);
+
 /* ---- argmax: lowest index on ties (elementwise.cu:103-104, :111-112).
  * margin[m] = best - second best (distinct indices), for near-tie reporting. */
 void or_argmax_rows_f64(const double* v, int rows, int n, int32_t* idx, double* margin);

@@ -25,6 +25,7 @@ _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
 
@@ -71,6 +72,8 @@ def lib():
     L.or_argmax_rows_f64.argtypes = [_f64p, i, i, _i32p, _f64p]
     L.or_argmax_rows_f32.argtypes = [_f32p, i, i, _i32p]
     L.or_argmax_rows_bf16.argtypes = [_u16p, i, i, _i32p]
+    L.or_w8_quantize.argtypes = [_u16p, i, i, i, _i8p, _u16p]
+    L.or_w8_matmul_f64.argtypes = [_u16p, i, _i8p, _u16p, i, i, i, _f64p, i]
     L.or_f32_to_bf16.argtypes = [C.c_float]
     L.or_f32_to_bf16.restype = C.c_uint16
     _lib = L
@@ -237,6 +240,28 @@ def matmul_f64(x, q, zp, s, group=128, round_w=False, threads=None):
     fn = lib().or_matmul_bf16w_f64 if round_w else lib().or_matmul_f64
     fn(x, M, _c(q, np.uint8), _c(zp, np.uint8), _c(s, np.uint16), N, K, group, y,
        threads or nthreads())
+    return y
+
+
+def w8_quantize(w_bf16, group=128):
+    """W8A16 quantizer (k_quant_w8, gemv_w4a16.cu:478-495): bf16 [N][K] ->
+    (q int8 [N][K], s bf16 bits [N][G])."""
+    w = _c(w_bf16, np.uint16)
+    N, K = w.shape
+    q = np.empty((N, K), np.int8)
+    s = np.empty((N, K // group), np.uint16)
+    lib().or_w8_quantize(w, N, K, group, q, s)
+    return q, s
+
+
+def w8_matmul_f64(x, q, s, group=128, threads=None):
+    """fp64 y = x @ (q * s)^T for W8A16 weights."""
+    x = _c(np.atleast_2d(x), np.uint16)
+    M, K = x.shape
+    N = q.shape[0]
+    y = np.empty((M, N), np.float64)
+    lib().or_w8_matmul_f64(x, M, _c(q, np.int8), _c(s, np.uint16), N, K, group, y,
+                           threads or nthreads())
     return y
 
 

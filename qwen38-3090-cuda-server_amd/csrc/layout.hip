@@ -112,6 +112,85 @@ __global__ void k_dequant_rows(uint16_t* __restrict__ dst, const uint32_t* __res
   *reinterpret_cast<u32x4*>(dst + (size_t)r * K + 8 * wi) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// ------------------------------------------------------------ 8-bit weights
+// W8A16 quantizer, the reference's k_quant_w8 (src/kernels/gemv_w4a16.cu:478-495)
+// writing the 8-bit block layout directly: one thread per (row n, group g);
+// mx = max |w|, s = bf16(mx / 127), q = clamp(rint(w * (127 / mx)), +-127),
+// stored as u = q + 128 at [tile][g][j][position][32 B], j = k / 32 in the group.
+__global__ void k_w8_quantize(uint8_t* __restrict__ qw, uint16_t* __restrict__ sc,
+                              const uint16_t* __restrict__ src, int N, int K, int G) {
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long long)N * G) return;
+  const int n = (int)(t / G), g = (int)(t % G);
+  const u32x4* row = reinterpret_cast<const u32x4*>(src + (size_t)n * K + (size_t)g * kGroup);
+  float mx = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const u32x4 v = row[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      mx = fmaxf(mx, fabsf(bf16_bits_to_f32(v[e] & 0xffffu)));
+      mx = fmaxf(mx, fabsf(bf16_bits_to_f32(v[e] >> 16)));
+    }
+  }
+  const float inv = mx > 0.f ? 127.0f / mx : 0.f;
+  const int b = n >> 6, rr = n & 63;
+  const size_t blk = (size_t)b * G + g;
+  sc[blk * 64 + rr] = to_bf16(mx / 127.0f);
+  uint8_t* dst = qw + blk * 8192 + tile_pos_of_row(rr) * 32;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = row[4 * j + i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int hlf = 0; hlf < 2; ++hlf) {
+          const float w = bf16_bits_to_f32(hlf ? (v[e] >> 16) : (v[e] & 0xffffu));
+          int q = (int)__builtin_rintf(w * inv);
+          q = q < -127 ? -127 : (q > 127 ? 127 : q);
+          pair |= (uint32_t)(q + 128) << (8 * hlf);
+        }
+        // bytes 8i + 2e, 8i + 2e + 1 of the 32-byte chunk
+        const int byte = 8 * i + 2 * e;
+        if ((byte & 3) == 0)
+          o[byte >> 2] = pair;
+        else
+          o[byte >> 2] |= pair << 16;
+      }
+    }
+    u32x4* d = reinterpret_cast<u32x4*>(dst + (size_t)j * 2048);
+    d[0] = u32x4{o[0], o[1], o[2], o[3]};
+    d[1] = u32x4{o[4], o[5], o[6], o[7]};
+  }
+}
+
+// dst [nrows][K] = RNE(q * s) of 8-bit weights, one thread per 8 consecutive k.
+__global__ void k_w8_dequant_rows(uint16_t* __restrict__ dst, const uint8_t* __restrict__ qw,
+                                  const uint16_t* __restrict__ sc, int row0, int nrows, int K,
+                                  int G) {
+  const int cpr = K / 8;
+  const size_t t = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (size_t)nrows * cpr) return;
+  const int r = (int)(t / cpr), ci = (int)(t % cpr);
+  const int n = row0 + r, b = n >> 6, rr = n & 63;
+  const int g = ci >> 4, j = (ci >> 2) & 3, e8 = ci & 3;
+  const size_t blk = (size_t)b * G + g;
+  const u32x2 v = *reinterpret_cast<const u32x2*>(qw + blk * 8192 + (size_t)j * 2048 +
+                                                  tile_pos_of_row(rr) * 32 + e8 * 8);
+  const float s = bf16_bits_to_f32(sc[blk * 64 + rr]);
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t w = v[k >> 1] >> (16 * (k & 1));
+    o[k] = pack_bf16x2((float)((int)(w & 0xffu) - 128) * s, (float)((int)((w >> 8) & 0xffu) - 128) * s);
+  }
+  *reinterpret_cast<u32x4*>(dst + (size_t)r * K + 8 * ci) = u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // --------------------------------------------------------------- generator
 // Counter-based synthetic inputs (identical spec in the CPU test oracle):
 //   key = mix64(seed * 0xD1B54A32D192ED03 + stream_id)
@@ -356,6 +435,65 @@ int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows, v
   const size_t n = (size_t)nrows * (w->in_f / 8);
   k_dequant_rows<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
       dst, w->qweight, w->scale, w->zeros, row0, nrows, w->in_f, w->num_groups);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_w8_quantize(qw4_w8_weights* w, const uint16_t* src, int out_f, int in_f,
+                    int group_size, void* stream) {
+  if (!w || !src) return QW4_ERR_NULL;
+  std::memset(w, 0, sizeof(*w));
+  if (group_size != kGroup) return QW4_ERR_GROUP;
+  if (out_f <= 0 || out_f % kTileN || in_f <= 0 || in_f % kGroup) return QW4_ERR_SHAPE;
+  if ((size_t)out_f * in_f >= (1ull << 32)) return QW4_ERR_SHAPE;
+  if ((uintptr_t)src & 15) return QW4_ERR_ALIGN;
+  const int G = in_f / kGroup;
+  hipError_t e = hipMalloc((void**)&w->qweight, (size_t)out_f * in_f);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->scale, (size_t)out_f * G * 2);
+  if (e != hipSuccess) {
+    set_hip_error((int)e);
+    (void)hipGetLastError();
+    if (w->qweight) (void)hipFree(w->qweight);
+    if (w->scale) (void)hipFree(w->scale);
+    std::memset(w, 0, sizeof(*w));
+    return QW4_ERR_NOMEM;
+  }
+  w->out_f = out_f;
+  w->in_f = in_f;
+  w->group_size = group_size;
+  w->num_groups = G;
+  const size_t n = (size_t)out_f * G;
+  k_w8_quantize<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(w->qweight, w->scale, src,
+                                                                    out_f, in_f, G);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_w8_free(qw4_w8_weights* w) {
+  if (!w) return QW4_ERR_NULL;
+  if (w->qweight) (void)hipFree(w->qweight);
+  if (w->scale) (void)hipFree(w->scale);
+  std::memset(w, 0, sizeof(*w));
+  return QW4_OK;
+}
+
+size_t qw4_w8_bytes(const qw4_w8_weights* w) {
+  if (!w) return 0;
+  return (size_t)w->out_f * w->in_f + (size_t)w->out_f * w->num_groups * 2;
+}
+
+int qw4_w8_dequant_rows(uint16_t* dst, const qw4_w8_weights* w, int row0, int nrows,
+                        void* stream) {
+  if (!dst || !w || !w->qweight || !w->scale) return QW4_ERR_NULL;
+  if (w->group_size != kGroup || w->out_f % kTileN || w->in_f % kGroup ||
+      w->num_groups != w->in_f / kGroup)
+    return QW4_ERR_SHAPE;
+  if (row0 < 0 || nrows < 0 || row0 + nrows > w->out_f) return QW4_ERR_SHAPE;
+  if (((uintptr_t)dst & 15) != 0) return QW4_ERR_ALIGN;
+  if (nrows == 0) return QW4_OK;
+  const size_t n = (size_t)nrows * (w->in_f / 8);
+  k_w8_dequant_rows<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
+      dst, w->qweight, w->scale, row0, nrows, w->in_f, w->num_groups);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
 }

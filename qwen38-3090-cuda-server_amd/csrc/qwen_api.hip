@@ -48,6 +48,17 @@ void mirror(GemvScratch& s) {
   s.max_m = s.impl.max_m;
 }
 
+qw4_w8_weights view8(const W8A16Weights& w) {
+  qw4_w8_weights v;
+  v.qweight = reinterpret_cast<uint8_t*>(w.qweight);
+  v.scale = reinterpret_cast<uint16_t*>(w.scale);
+  v.out_f = w.out_f;
+  v.in_f = w.in_f;
+  v.group_size = w.group_size;
+  v.num_groups = w.num_groups;
+  return v;
+}
+
 const uint16_t* u16(const __hip_bfloat16* p) { return reinterpret_cast<const uint16_t*>(p); }
 uint16_t* u16(__hip_bfloat16* p) { return reinterpret_cast<uint16_t*>(p); }
 
@@ -144,6 +155,48 @@ void gemv_argmax_w4a16(int32_t* idx, const W4A16Weights& w, const __hip_bfloat16
                        GemvScratch& s, hipStream_t stream) {
   const qw4_weights v = view(w);
   check(qw4_gemv_argmax(idx, &v, u16(x), M, &s.impl, stream), "gemv_argmax_w4a16");
+}
+
+void quantize_w8a16(W8A16Weights& dst, const __hip_bfloat16* src, int out_f, int in_f,
+                    int group_size, hipStream_t stream) {
+  qw4_w8_weights v{};
+  check(qw4_w8_quantize(&v, u16(src), out_f, in_f, group_size, stream), "quantize_w8a16");
+  dst.qweight = reinterpret_cast<int8_t*>(v.qweight);
+  dst.scale = reinterpret_cast<__hip_bfloat16*>(v.scale);
+  dst.out_f = v.out_f;
+  dst.in_f = v.in_f;
+  dst.group_size = v.group_size;
+  dst.num_groups = v.num_groups;
+}
+
+void gemv_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,
+                GemvScratch& s, hipStream_t stream) {
+  const qw4_w8_weights v = view8(w);
+  check(qw4_w8_gemv(u16(y), &v, u16(x), &s.impl, stream), "gemv_w8a16");
+}
+
+void gemm_small_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,
+                      int M, GemvScratch& s, hipStream_t stream) {
+  const qw4_w8_weights v = view8(w);
+  check(qw4_w8_gemm_small(u16(y), &v, u16(x), M, &s.impl, stream), "gemm_small_w8a16");
+}
+
+void gemv_argmax_w8a16(int32_t* idx, const W8A16Weights& w, const __hip_bfloat16* x, int M,
+                       GemvScratch& s, hipStream_t stream) {
+  const qw4_w8_weights v = view8(w);
+  check(qw4_w8_gemv_argmax(idx, &v, u16(x), M, &s.impl, stream), "gemv_argmax_w8a16");
+}
+
+void w8a16_dequant_rows(__hip_bfloat16* dst, const W8A16Weights& w, int row0, int nrows,
+                        hipStream_t stream) {
+  const qw4_w8_weights v = view8(w);
+  check(qw4_w8_dequant_rows(u16(dst), &v, row0, nrows, stream), "w8a16_dequant_rows");
+}
+
+void w8a16_free(W8A16Weights& w) {
+  qw4_w8_weights v = view8(w);
+  check(qw4_w8_free(&v), "w8a16_free");
+  w = W8A16Weights{};
 }
 
 void gemm_workspace_alloc(GemmWorkspace& ws, size_t bytes) {

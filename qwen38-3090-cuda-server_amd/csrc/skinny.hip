@@ -90,6 +90,7 @@ struct SkinnyArgs {
   uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
   int M, N, K, G, tiles, max_tiles, P, U;
   uint32_t slot_bytes;
+  uint32_t weight_bytes;   // packed weights (4- or 8-bit blocks)
 };
 
 // Monotonic key: larger value first, then lower index (elementwise.cu:103-104).
@@ -146,12 +147,13 @@ struct SkinnyRsrc {
 
 __device__ __forceinline__ SkinnyRsrc skinny_rsrc(const SkinnyArgs& a) {
   SkinnyRsrc r;
-  r.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0,
-                                           (int)((uint32_t)a.N * (uint32_t)a.K / 2u), 0x00020000);
+  r.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0, (int)a.weight_bytes,
+                                           0x00020000);
   r.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0,
                                            (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
   r.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
-                                           (int)((uint32_t)a.N * (uint32_t)a.G / 2u), 0x00020000);
+                                           a.zr ? (int)((uint32_t)a.N * (uint32_t)a.G / 2u) : 0,
+                                           0x00020000);
   r.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x), 0,
                                           (int)((uint32_t)a.M * (uint32_t)a.K * 2u), 0x00020000);
   return r;
@@ -198,6 +200,99 @@ __device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, N
     for (int jj = 0; jj < 4; ++jj) acc[st][jj] += sf * (C[st][jj] - zf * Cs[jj]);
   }
 }
+
+// ------------------------------------------------------- 8-bit weights
+// W8A16 (the reference's lm_head format, gemv_w4a16.cuh:141-166): per (row,
+// 128-group) a bf16 scale and int8 q in [-127, 127], stored as the byte
+// u = q + 128. Block = (64-row tile, group), 8 KiB: [4 j][64 p][32 B], position
+// p holding row 4 (p % 16) + p / 16 as in the 4-bit layout, chunk j covering
+// k = 128 g + 32 j + [0, 32) in natural byte order. A byte is an exact bf16
+// (u <= 255 needs 8 significant bits); the offset is removed like the 4-bit
+// zero point: acc += s (C - 128 S_m), with S_m from the ones operand.
+struct GroupData8 {
+  u32x4 w[4][2];   // row quad st -> 32 bytes (k 32q .. 32q + 31)
+  u32x4 x[4];
+  u32x2 s;
+};
+
+__device__ __forceinline__ void load_group8(GroupData8& d, const SkinnyRsrc& r,
+                                            const SkinnyArgs& a, int b, int g, int c,
+                                            uint32_t woff, uint32_t xoff) {
+  const uint32_t blk = (uint32_t)b * (uint32_t)a.G + (uint32_t)g;
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      d.w[st][h] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + st * 512 + h * 16,
+                                                         blk * 8192u, 0);
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    d.x[t] = __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
+  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * 128u, 0);
+}
+
+// Eight bytes -> eight bf16 values (exact).
+__device__ __forceinline__ bf16x8 bytes8_bf16(uint32_t lo, uint32_t hi) {
+  u32x4 o;
+  o[0] = pack_bf16x2((float)(lo & 0xffu), (float)((lo >> 8) & 0xffu));
+  o[1] = pack_bf16x2((float)((lo >> 16) & 0xffu), (float)(lo >> 24));
+  o[2] = pack_bf16x2((float)(hi & 0xffu), (float)((hi >> 8) & 0xffu));
+  o[3] = pack_bf16x2((float)((hi >> 16) & 0xffu), (float)(hi >> 24));
+  return __builtin_bit_cast(bf16x8, o);
+}
+
+__device__ __forceinline__ void mma_group8(f32x4 (&acc)[4], const GroupData8& d) {
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
+                                                       0x3F803F80u, 0x3F803F80u});
+  f32x4 C[4], Cs;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const bf16x8 A = __builtin_bit_cast(bf16x8, d.x[t]);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const u32x4 v = d.w[st][t >> 1];
+      const bf16x8 B = bytes8_bf16(v[(t & 1) * 2], v[(t & 1) * 2 + 1]);
+      C[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          A, B, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : C[st], 0, 0, 0);
+    }
+    Cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones,
+                                                 t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Cs,
+                                                 0, 0, 0);
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const uint32_t sbits = (st & 1) ? (d.s[st >> 1] >> 16) : (d.s[st >> 1] & 0xffffu);
+    const float sf = bf16_bits_to_f32(sbits);
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) acc[st][jj] += sf * (C[st][jj] - 128.0f * Cs[jj]);
+  }
+}
+
+// The two block formats behind one kernel.
+template <int FMT>
+struct Fmt;
+template <>
+struct Fmt<4> {
+  using Data = GroupData;
+  static constexpr uint32_t kBlockBytes = 4096;
+  __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 1024 + c * 16); }
+  __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
+                              int c, uint32_t woff, uint32_t xoff) {
+    load_group(d, r, a, b, g, c, woff, xoff);
+  }
+  __device__ static void mma(f32x4 (&acc)[4], const Data& d, NibConst k) { mma_group(acc, d, k); }
+};
+template <>
+struct Fmt<8> {
+  using Data = GroupData8;
+  static constexpr uint32_t kBlockBytes = 8192;
+  __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 2048 + c * 32); }
+  __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
+                              int c, uint32_t woff, uint32_t xoff) {
+    load_group8(d, r, a, b, g, c, woff, xoff);
+  }
+  __device__ static void mma(f32x4 (&acc)[4], const Data& d, NibConst) { mma_group8(acc, d); }
+};
 
 // ------------------------------------------------------------- epilogues
 // Running argmax of one workgroup: per lane, the best (value, column) of rows
@@ -401,7 +496,7 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
 // lo + wave + W, ... in batches of two blocks (one for W = 16, to fit 128
 // VGPRs). W = 4: LDS sums double-buffered per segment; W >= 8: one buffer and
 // a second barrier.
-template <int OUT, int W, bool M1>
+template <int OUT, int W, bool M1, int FMT>
 __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   constexpr int kNbuf = W == 4 ? 2 : 1;
   constexpr int kBatch = W == 16 ? 1 : 2;
@@ -410,7 +505,7 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int c = lane & 15, q = lane >> 4;
   const SkinnyRsrc rs = skinny_rsrc(a);
-  const uint32_t woff = (uint32_t)(q * 1024 + c * 16);
+  const uint32_t woff = Fmt<FMT>::woff(q, c);
   const uint32_t xoff = (uint32_t)(c * a.K + 32 * q) * 2u;
   const int p = blockIdx.x;
   const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
@@ -432,12 +527,12 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
 #pragma unroll
     for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
     for (int g = lo + wave; g < hi; g += kBatch * W) {
-      GroupData d0, d1;
+      typename Fmt<FMT>::Data d0, d1;
       const bool two = kBatch == 2 && g + W < hi;
-      load_group(d0, rs, a, sb, g, c, woff, xoff);
-      if (two) load_group(d1, rs, a, sb, g + W, c, woff, xoff);
-      mma_group(acc, d0, k);
-      if (two) mma_group(acc, d1, k);
+      Fmt<FMT>::load(d0, rs, a, sb, g, c, woff, xoff);
+      if (two) Fmt<FMT>::load(d1, rs, a, sb, g + W, c, woff, xoff);
+      Fmt<FMT>::mma(acc, d0, k);
+      if (two) Fmt<FMT>::mma(acc, d1, k);
     }
     // Sum the segment over the W waves in wave order.
     if (wave) {
@@ -497,7 +592,7 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
 int g_env_wgs = 0, g_env_tiles_per_wg = 0, g_env_w = 0;
 std::once_flag g_env_once;
 int g_cus[64] = {0};
-int g_occ[64][3][3][2] = {{{{0}}}};
+int g_occ[64][3][3][2][2] = {{{{{0}}}}};
 
 void read_env() {
   std::call_once(g_env_once, [] {
@@ -529,14 +624,15 @@ int device_cus() {
   return g_cus[dev];
 }
 
-template <int OUT, int W, bool M1>
+template <int OUT, int W, bool M1, int FMT>
 int wgs_per_cu() {
   read_env();
   if (g_env_wgs) return g_env_wgs;
-  int& slot = g_occ[current_device()][OUT][W == 4 ? 0 : (W == 8 ? 1 : 2)][M1 ? 1 : 0];
+  int& slot =
+      g_occ[current_device()][OUT][W == 4 ? 0 : (W == 8 ? 1 : 2)][M1 ? 1 : 0][FMT == 8 ? 1 : 0];
   if (!slot) {
     int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_skinny<OUT, W, M1>, 64 * W, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_skinny<OUT, W, M1, FMT>, 64 * W, 0) !=
             hipSuccess ||
         n <= 0)
       n = 1;
@@ -553,7 +649,7 @@ struct Launch {
 // (measured on MI355X: the 19 MB qkv and 11 MB o projections) do better with
 // more waves per tile and fewer split tiles: M = 1 uses W = 16 with two
 // workgroups per tile, M > 1 W = 8 with one.
-template <int OUT, bool M1>
+template <int OUT, bool M1, int FMT = 4>
 Launch launch_for(int out_f, int G) {
   read_env();
   const int tiles = out_f / kTileN;
@@ -564,7 +660,7 @@ Launch launch_for(int out_f, int G) {
   if (g_env_w == 4 || g_env_w == 8 || g_env_w == 16) l.W = g_env_w;
   long long cap;
   if (l.W == 4)
-    cap = (long long)device_cus() * wgs_per_cu<OUT, 4, M1>();
+    cap = (long long)device_cus() * wgs_per_cu<OUT, 4, M1, FMT>();
   else
     cap = (long long)tiles * (l.W == 16 ? 2 : 1);
   if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
@@ -579,43 +675,50 @@ Launch launch_for(int out_f, int G) {
   return l;
 }
 
-template <int OUT, bool M1>
+template <int OUT, bool M1, int FMT>
 void launch(const SkinnyArgs& a, int W, hipStream_t st) {
   if (W == 16)
-    k_skinny<OUT, 16, M1><<<a.P, 1024, 0, st>>>(a);
+    k_skinny<OUT, 16, M1, FMT><<<a.P, 1024, 0, st>>>(a);
   else if (W == 8)
-    k_skinny<OUT, 8, M1><<<a.P, 512, 0, st>>>(a);
+    k_skinny<OUT, 8, M1, FMT><<<a.P, 512, 0, st>>>(a);
   else
-    k_skinny<OUT, 4, M1><<<a.P, 256, 0, st>>>(a);
+    k_skinny<OUT, 4, M1, FMT><<<a.P, 256, 0, st>>>(a);
 }
 
 // Scratch regions inside qw4_scratch.partial: slots for the largest grid, then
 // the fixed-point words of every tile.
 size_t slot_floats() { return (size_t)device_cus() * kMaxWgsPerCu * 2 * 1024; }
 
-template <int OUT>
-int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scratch* s,
+// The packed weights of either format, as the kernel sees them.
+struct WeightView {
+  const void* qw;
+  const uint16_t* sc;
+  const uint16_t* zr;   // 4-bit zero points; null for 8-bit
+  int out_f, in_f, G;
+  size_t weight_bytes;
+};
+
+template <int OUT, int FMT>
+int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scratch* s,
                void* stream) {
-  int st = check_weights_public(w);
-  if (st) return st;
   if (!y || !x || !s || !s->counters || !s->partial || !s->keys) return QW4_ERR_NULL;
   if (M < 1 || M > 16) return QW4_ERR_M;
   if (((uintptr_t)x & 15) || ((uintptr_t)y & (OUT == OUT_F32 ? 15 : (OUT == OUT_BF16 ? 7 : 3))))
     return QW4_ERR_ALIGN;
-  const int tiles = w->out_f / kTileN;
-  if (tiles > s->max_tiles || M > s->max_m || w->in_f > s->max_in) return QW4_ERR_SCRATCH;
+  const int tiles = w.out_f / kTileN;
+  if (tiles > s->max_tiles || M > s->max_m || w.in_f > s->max_in) return QW4_ERR_SCRATCH;
   // loads address weights and x through 32-bit buffer offsets
-  if ((size_t)w->out_f * w->in_f / 2 >= (1ull << 32)) return QW4_ERR_SHAPE;
+  if (w.weight_bytes >= (1ull << 32)) return QW4_ERR_SHAPE;
   const bool m1 = M == 1;
-  const Launch l = m1 ? launch_for<OUT, true>(w->out_f, w->num_groups)
-                      : launch_for<OUT, false>(w->out_f, w->num_groups);
+  const Launch l = m1 ? launch_for<OUT, true, FMT>(w.out_f, w.G)
+                      : launch_for<OUT, false, FMT>(w.out_f, w.G);
   if ((size_t)l.P * 2 * 1024 > slot_floats() ||
       slot_floats() + (size_t)tiles * 64 * 2 > s->partial_elems)
     return QW4_ERR_SCRATCH;
   SkinnyArgs a;
-  a.qw = w->qweight;
-  a.sc = w->scale;
-  a.zr = w->zeros;
+  a.qw = static_cast<const uint32_t*>(w.qw);
+  a.sc = w.sc;
+  a.zr = w.zr;
   a.x = x;
   a.y = y;
   a.slots = s->partial;
@@ -623,20 +726,50 @@ int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scra
   a.counters = s->counters;
   a.keys = s->keys;
   a.M = M;
-  a.N = w->out_f;
-  a.K = w->in_f;
-  a.G = w->num_groups;
+  a.N = w.out_f;
+  a.K = w.in_f;
+  a.G = w.G;
   a.tiles = tiles;
   a.max_tiles = s->max_tiles;
   a.P = l.P;
-  a.U = tiles * w->num_groups;
+  a.U = tiles * w.G;
   a.slot_bytes = (uint32_t)(slot_floats() * 4);
+  a.weight_bytes = (uint32_t)w.weight_bytes;
   if (m1)
-    launch<OUT, true>(a, l.W, (hipStream_t)stream);
+    launch<OUT, true, FMT>(a, l.W, (hipStream_t)stream);
   else
-    launch<OUT, false>(a, l.W, (hipStream_t)stream);
+    launch<OUT, false, FMT>(a, l.W, (hipStream_t)stream);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
+}
+
+template <int OUT>
+int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scratch* s,
+               void* stream) {
+  const int st = check_weights_public(w);
+  if (st) return st;
+  const WeightView v{w->qweight, w->scale, w->zeros, w->out_f, w->in_f, w->num_groups,
+                     (size_t)w->out_f * w->in_f / 2};
+  return run_skinny<OUT, 4>(y, v, x, M, s, stream);
+}
+
+int check_w8(const qw4_w8_weights* w) {
+  if (!w || !w->qweight || !w->scale) return QW4_ERR_NULL;
+  if (w->group_size != kGroup) return QW4_ERR_GROUP;
+  if (w->out_f <= 0 || w->out_f % kTileN || w->in_f <= 0 || w->in_f % kGroup ||
+      w->num_groups != w->in_f / kGroup)
+    return QW4_ERR_SHAPE;
+  return QW4_OK;
+}
+
+template <int OUT>
+int run_skinny8(void* y, const qw4_w8_weights* w, const uint16_t* x, int M, qw4_scratch* s,
+                void* stream) {
+  const int st = check_w8(w);
+  if (st) return st;
+  const WeightView v{w->qweight, w->scale, nullptr, w->out_f, w->in_f, w->num_groups,
+                     (size_t)w->out_f * w->in_f};
+  return run_skinny<OUT, 8>(y, v, x, M, s, stream);
 }
 
 }  // namespace
@@ -726,6 +859,21 @@ int qw4_gemm_mma(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
 int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
                     qw4_scratch* s, void* stream) {
   return run_skinny<OUT_ARGMAX>(idx, w, x, M, s, stream);
+}
+
+int qw4_w8_gemv(uint16_t* y, const qw4_w8_weights* w, const uint16_t* x, qw4_scratch* s,
+                void* stream) {
+  return run_skinny8<OUT_BF16>(y, w, x, 1, s, stream);
+}
+
+int qw4_w8_gemm_small(uint16_t* y, const qw4_w8_weights* w, const uint16_t* x, int M,
+                      qw4_scratch* s, void* stream) {
+  return run_skinny8<OUT_BF16>(y, w, x, M, s, stream);
+}
+
+int qw4_w8_gemv_argmax(int32_t* idx, const qw4_w8_weights* w, const uint16_t* x, int M,
+                       qw4_scratch* s, void* stream) {
+  return run_skinny8<OUT_ARGMAX>(idx, w, x, M, s, stream);
 }
 
 }  // extern "C"

@@ -42,6 +42,8 @@ EXPORTS = (
     "qw4_gemm", "qw4_argmax", "qw4_argmax_rows", "qw4_gen_bf16", "qw4_gen_awq_k",
     "qw4_stream_read", "qw4_st_open", "qw4_st_open_dir", "qw4_st_close", "qw4_st_count",
     "qw4_st_find", "qw4_st_last_error", "qw4_load_ct_fused",
+    "qw4_w8_quantize", "qw4_w8_free", "qw4_w8_bytes", "qw4_w8_dequant_rows", "qw4_w8_gemv",
+    "qw4_w8_gemm_small", "qw4_w8_gemv_argmax",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -71,6 +73,16 @@ class W4A16Weights(C.Structure):
 
     def total_bytes(self) -> int:
         return lib().qw4_weights_bytes(C.byref(self))
+
+
+class W8A16Weights(C.Structure):
+    """qw4_w8_weights / the reference's W8A16Weights (gemv_w4a16.cuh:147-154)."""
+    _fields_ = [("qweight", C.c_void_p), ("scale", C.c_void_p),
+                ("out_f", C.c_int32), ("in_f", C.c_int32), ("group_size", C.c_int32),
+                ("num_groups", C.c_int32)]
+
+    def total_bytes(self) -> int:
+        return lib().qw4_w8_bytes(C.byref(self))
 
 
 class GemvScratch(C.Structure):
@@ -104,6 +116,7 @@ def lib():
     L = C.CDLL(LIB_PATH)
     vp, i, sz, u64 = C.c_void_p, C.c_int, C.c_size_t, C.c_uint64
     W, S, WS = C.POINTER(W4A16Weights), C.POINTER(GemvScratch), C.POINTER(GemmWorkspace)
+    W8 = C.POINTER(W8A16Weights)
     sig = {
         "qw4_status_string": ([i], C.c_char_p),
         "qw4_last_hip_error": ([], i),
@@ -139,6 +152,13 @@ def lib():
         "qw4_st_find": ([vp, C.c_char_p, C.POINTER(StTensor)], i),
         "qw4_st_last_error": ([], C.c_char_p),
         "qw4_load_ct_fused": ([W, vp, C.POINTER(C.c_char_p), i, i, i, vp], i),
+        "qw4_w8_quantize": ([W8, vp, i, i, i, vp], i),
+        "qw4_w8_free": ([W8], i),
+        "qw4_w8_bytes": ([W8], sz),
+        "qw4_w8_dequant_rows": ([vp, W8, i, i, vp], i),
+        "qw4_w8_gemv": ([vp, W8, vp, S, vp], i),
+        "qw4_w8_gemm_small": ([vp, W8, vp, i, S, vp], i),
+        "qw4_w8_gemv_argmax": ([vp, W8, vp, i, S, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -302,6 +322,51 @@ def gemv_argmax_w4a16(idx, w: W4A16Weights, x, M: int, s: GemvScratch, stream=No
     _need(x, max(M, 0) * w.in_f * 2, "gemv_argmax_w4a16 x")
     _chk(lib().qw4_gemv_argmax(_ptr(idx), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
          "gemv_argmax_w4a16")
+
+
+# ------------------------------------------------------- 8-bit lm_head
+def quantize_w8a16(src, out_f: int, in_f: int, group_size: int = 128, stream=None) -> W8A16Weights:
+    """quantize_w8a16 (gemv_w4a16.cuh:156-157): bf16 [out_f][in_f] -> 8-bit weights."""
+    _need(src, out_f * in_f * 2, "quantize_w8a16 src")
+    w = W8A16Weights()
+    _chk(lib().qw4_w8_quantize(C.byref(w), _ptr(src), out_f, in_f, group_size, _stream(stream)),
+         "quantize_w8a16")
+    return w
+
+
+def w8a16_free(w: W8A16Weights) -> None:
+    """w8a16_free (gemv_w4a16.cuh:166)."""
+    _chk(lib().qw4_w8_free(C.byref(w)), "w8a16_free")
+
+
+def w8a16_dequant_rows(dst, w: W8A16Weights, row0: int, nrows: int, stream=None) -> None:
+    _need(dst, max(nrows, 0) * w.in_f * 2, "w8a16_dequant_rows dst")
+    _chk(lib().qw4_w8_dequant_rows(_ptr(dst), C.byref(w), row0, nrows, _stream(stream)),
+         "w8a16_dequant_rows")
+
+
+def gemv_w8a16(y, w: W8A16Weights, x, s: GemvScratch, stream=None) -> None:
+    """gemv_w8a16 (gemv_w4a16.cuh:158-159)."""
+    _need(y, w.out_f * 2, "gemv_w8a16 y")
+    _need(x, w.in_f * 2, "gemv_w8a16 x")
+    _chk(lib().qw4_w8_gemv(_ptr(y), C.byref(w), _ptr(x), C.byref(s), _stream(stream)),
+         "gemv_w8a16")
+
+
+def gemm_small_w8a16(y, w: W8A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """gemm_small_w8a16 (gemv_w4a16.cuh:163-164)."""
+    _need(y, max(M, 0) * w.out_f * 2, "gemm_small_w8a16 y")
+    _need(x, max(M, 0) * w.in_f * 2, "gemm_small_w8a16 x")
+    _chk(lib().qw4_w8_gemm_small(_ptr(y), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
+         "gemm_small_w8a16")
+
+
+def gemv_argmax_w8a16(idx, w: W8A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """8-bit lm_head + fused fp32 row-argmax (model.cu:796-815, lm_head_bits 8)."""
+    _need(idx, max(M, 0) * 4, "gemv_argmax_w8a16 idx")
+    _need(x, max(M, 0) * w.in_f * 2, "gemv_argmax_w8a16 x")
+    _chk(lib().qw4_w8_gemv_argmax(_ptr(idx), C.byref(w), _ptr(x), M, C.byref(s),
+                                  _stream(stream)), "gemv_argmax_w8a16")
 
 
 def gemm_w4a16(Cm, w: W4A16Weights, A, M: int, ws: GemmWorkspace | None = None, stream=None) -> None:

@@ -65,3 +65,18 @@ def weights_buffers(w, N: int, K: int):
         torch.cuda.synchronize()
         out.append(buf.cpu().numpy())
     return out
+
+
+def download(ptr: int, nbytes: int) -> np.ndarray:
+    """Copy nbytes of device memory at a raw pointer to a host uint8 array."""
+    import ctypes as C
+
+    import torch
+
+    buf = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    torch.cuda.synchronize()
+    hipMemcpy = C.CDLL("libamdhip64.so").hipMemcpy
+    hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    assert hipMemcpy(buf.data_ptr(), ptr, nbytes, 3) == 0   # device to device
+    torch.cuda.synchronize()
+    return buf.cpu().numpy()

@@ -234,3 +234,79 @@ def test_argmax_lowest_index_on_ties(orc):
     assert list(orc.argmax_rows_f32(f)) == list(np.argmax(f, axis=1))
     b = orc.f32_to_bf16(f)
     assert list(orc.argmax_rows_bf16(b)) == list(np.argmax(orc.bf16_to_f32(b), axis=1))
+
+
+# ------------------------------------------------------------------ W8A16
+def test_w8_quantize_recovers_power_of_two_grids(orc):
+    """Rows that are integer multiples k*c of a power of two c with max |k| =
+    127 quantize exactly: s = c and q = k (inv = 1/c is exact, so any sign,
+    index or rounding slip shows)."""
+    rng = np.random.default_rng(0)
+    N, K = 16, 512
+    k = rng.integers(-127, 128, (N, K))
+    c = 2.0 ** rng.integers(-12, 3, (N, K // 128))
+    k[:, ::128] = np.where(rng.random((N, K // 128)) < 0.5, 127, -127)   # pin the max
+    w = (k * np.repeat(c, 128, axis=1)).astype(np.float32)
+    q, s = orc.w8_quantize(orc.f32_to_bf16(w))
+    assert np.array_equal(q, k.astype(np.int8))
+    assert np.array_equal(orc.bf16_to_f32(s), c.astype(np.float32))
+
+
+def test_w8_quantize_properties(orc):
+    """Random bf16 rows: the group max maps to +-127, |q| <= 127, symmetric in
+    sign, zero groups give s = q = 0, and the reconstruction error is at most
+    half a step of the unrounded scale plus the bf16 rounding of the scale."""
+    rng = np.random.default_rng(1)
+    N, K = 32, 384
+    w = orc.f32_to_bf16(rng.standard_normal((N, K)).astype(np.float32) * 0.05)
+    w[3, 128:256] = 0                        # one all-zero group
+    q, s = orc.w8_quantize(w)
+    qn, sn = orc.w8_quantize(w ^ np.uint16(0x8000))   # negated source
+    assert np.array_equal(qn, -q) and np.array_equal(sn, s)
+    assert np.abs(q.astype(int)).max() <= 127
+    wf = orc.bf16_to_f32(w).reshape(N, 3, 128)
+    qg = q.reshape(N, 3, 128).astype(int)
+    for n in range(N):
+        for g in range(3):
+            mx = np.abs(wf[n, g]).max()
+            if mx == 0:
+                assert s[n, g] == 0 and not qg[n, g].any()
+                continue
+            assert np.abs(qg[n, g])[np.abs(wf[n, g]) == mx].min() == 127
+            step = mx / 127.0
+            err = np.abs(wf[n, g] - qg[n, g] * orc.bf16_to_f32(s[n, g]))
+            assert err.max() <= 0.5 * step * (1 + 1e-6) + 127 * abs(orc.bf16_to_f32(s[n, g]) - step)
+
+
+def test_w8_quantize_rounds_half_to_even(orc):
+    """w = (j + 1/2) * c for a power of two c with 127 c as the group max:
+    rint sends the halves to the even neighbour (the reference's __float2int_rn)."""
+    K = 128
+    c = 2.0 ** -6
+    row = np.zeros(K, np.float32)
+    row[0] = 127 * c
+    halves = np.arange(-60, 60) + 0.5
+    row[1:1 + halves.size] = halves * c
+    q, s = orc.w8_quantize(orc.f32_to_bf16(row[None, :]))
+    assert q[0, 0] == 127 and orc.bf16_to_f32(s[0, 0]) == c
+    want = np.rint(halves).astype(int)      # numpy rint: round half to even
+    assert np.array_equal(q[0, 1:1 + halves.size].astype(int), want)
+    assert all(v % 2 == 0 for v in want)
+
+
+def test_w8_matmul_closed_forms(orc):
+    """Column pick (x = e_k) returns q[:, k] * s; a constant x returns the row
+    sums; brute force in numpy float64 on a tiny shape."""
+    rng = np.random.default_rng(2)
+    N, K = 24, 256
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    s = orc.f32_to_bf16(np.abs(rng.standard_normal((N, 2)).astype(np.float32)) * 0.01)
+    sf = np.repeat(orc.bf16_to_f32(s).astype(np.float64), 128, axis=1)
+    x = np.zeros((1, K), np.uint16)
+    x[0, 77] = 0x3F80                                      # 1.0
+    assert np.array_equal(orc.w8_matmul_f64(x, q, s)[0], q[:, 77] * sf[:, 77])
+    ones = np.full((1, K), 0x3F80, np.uint16)
+    assert np.allclose(orc.w8_matmul_f64(ones, q, s)[0], (q * sf).sum(1), rtol=0, atol=1e-12)
+    xr = orc.f32_to_bf16(rng.standard_normal((3, K)).astype(np.float32))
+    ref = orc.bf16_to_f32(xr).astype(np.float64) @ (q * sf).T
+    assert np.allclose(orc.w8_matmul_f64(xr, q, s), ref, rtol=1e-12, atol=1e-12)
