@@ -585,6 +585,257 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
   if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
 }
 
+// ------------------------------------------------------ data-parallel rows
+// k_rows: workgroup p owns whole units [start(p), start(p + 1)); a unit is S
+// row quads st0 .. st0 + S - 1 of one tile (16 S rows: 4c + st for lanes c)
+// over all of K, split among the workgroup's W waves only and summed in LDS.
+// No workgroup exchanges partial sums with another, so nothing is waited on
+// at the end but the stores. Small units (S = 1: 16 rows) balance a launch
+// over the CUs where whole 64-row tiles cannot.
+// k_rows with activations in LDS: at most this many 16-byte chunks per thread
+// (M K 2 <= kRowsXChunks * 16 * 64 W bytes).
+constexpr int kRowsXChunks = 4;
+constexpr int kLdsBytes = 160 * 1024;   // LDS per CU on gfx950
+
+
+template <int FMT, int S, bool XL>
+struct RowsData {
+  u32x4 w[S][FMT == 8 ? 2 : 1];
+  u32x4 x[XL ? 1 : 4];       // activations (registers) unless they sit in LDS
+  uint32_t s[(S + 1) / 2];   // bf16 scales of rows 4c + st0 + i, two per word
+  uint32_t z;                // zero points of rows 4c .. 4c + 3 (4-bit)
+};
+
+template <int FMT, int S, bool XL>
+__device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyRsrc& r, uint32_t blk,
+                                          int g, uint32_t woff, uint32_t soff, uint32_t zoff,
+                                          uint32_t xoff) {
+  constexpr uint32_t kBlk = FMT == 8 ? 8192u : 4096u;
+  constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;   // bytes of one row quad in a chunk
+#pragma unroll
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int h = 0; h < (FMT == 8 ? 2 : 1); ++h)
+      d.w[i][h] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + i * kQuad + h * 16,
+                                                        blk * kBlk, 0);
+  if (!XL) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      d.x[t & (XL ? 0 : 3)] =
+          __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
+  }
+  if (S == 4) {
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r.sc, soff, blk * 128u, 0);
+    d.s[0] = v[0];
+    d.s[(S + 1) / 2 - 1] = v[1];
+  } else if (S == 2) {
+    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff, blk * 128u, 0);
+  } else {
+    d.s[0] = __builtin_amdgcn_raw_buffer_load_b16(r.sc, soff, blk * 128u, 0);
+  }
+  if (FMT == 4) d.z = __builtin_amdgcn_raw_buffer_load_b16(r.zr, zoff, blk * 32u, 0);
+}
+
+// XL: activations come from LDS (xl: this lane's row, k chunk q, group g);
+// otherwise from the registers rows_load filled.
+template <int FMT, int S, bool XL>
+__device__ __forceinline__ void rows_mma(f32x4 (&acc)[S], const RowsData<FMT, S, XL>& d, NibConst k,
+                                         int st0, const u32x4* xl) {
+  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
+                                                       0x3F803F80u, 0x3F803F80u});
+  f32x4 C[S], Cs;
+  u32x4 xr[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) xr[t] = XL ? xl[t] : d.x[t & (XL ? 0 : 3)];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const bf16x8 A = __builtin_bit_cast(bf16x8, xr[t]);
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+      bf16x8 B;
+      if (FMT == 4) {
+        B = nib8(d.w[i][0][t], k);
+      } else {
+        const u32x4 v = d.w[i][(t >> 1) & (FMT == 8 ? 1 : 0)];
+        B = bytes8_bf16(v[(t & 1) * 2], v[(t & 1) * 2 + 1]);
+      }
+      C[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+          A, B, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : C[i], 0, 0, 0);
+    }
+    Cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones,
+                                                 t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Cs,
+                                                 0, 0, 0);
+  }
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const uint32_t sbits = (d.s[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+    const float sf = bf16_bits_to_f32(sbits);
+    const float zf = FMT == 4 ? 128.0f + (float)((d.z >> (4 * (st0 + i))) & 0xFu) : 128.0f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) acc[i][jj] += sf * (C[i][jj] - zf * Cs[jj]);
+  }
+}
+
+// Final values of one unit (wave 0): rows m = 4q + jj, columns b*64 + 4c + st0 + i.
+template <int OUT, int S>
+__device__ __forceinline__ void emit_rows(const SkinnyArgs& a, int b, int st0,
+                                          const f32x4 (&acc)[S], int lane, Best& bs) {
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = b * kTileN + 4 * c + st0;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int m = 4 * q + jj;
+    if (OUT == OUT_ARGMAX) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) best_fold(bs, jj, acc[i][jj], n0 + i);
+      continue;
+    }
+    if (m >= a.M) continue;
+    if (OUT == OUT_BF16) {
+      uint16_t* y = static_cast<uint16_t*>(a.y) + (size_t)m * a.N + n0;
+      if (S == 4)
+        *reinterpret_cast<u32x2*>(y) = u32x2{pack_bf16x2(acc[0][jj], acc[1 % S][jj]),
+                                             pack_bf16x2(acc[2 % S][jj], acc[3 % S][jj])};
+      else if (S == 2)
+        *reinterpret_cast<uint32_t*>(y) = pack_bf16x2(acc[0][jj], acc[1 % S][jj]);
+      else
+        *y = to_bf16(acc[0][jj]);
+    } else {
+      float* y = static_cast<float*>(a.y) + (size_t)m * a.N + n0;
+#pragma unroll
+      for (int i = 0; i < S; ++i) y[i] = acc[i][jj];
+    }
+  }
+}
+
+// Each wave walks its items (unit u, group g), g = wave, wave + W, ... < G,
+// over the workgroup's units [start(p), start(p + 1)) in order, D items ahead
+// (the next loads are issued across unit boundaries too). Every wave closes
+// every unit: it writes its partial (zero if it had no item) to one of two LDS
+// buffers and passes one barrier, so the waves stay in step for any G; wave 0
+// then sums the W partials in wave order and emits the unit. No workgroup
+// depends on another.
+template <int OUT, int FMT, int S, int W, bool XL, int D>
+__global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
+  constexpr int kPer = 4 / S;   // units per tile
+  constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
+  __shared__ f32x4 red[2][W][S][64];
+  extern __shared__ u32x4 xlds[];
+  // wave-uniform (scalar) so the item cursors live in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const SkinnyRsrc rs = skinny_rsrc(a);
+  const uint32_t xoff = (uint32_t)(c * a.K + 32 * q) * 2u;
+  const uint32_t zoff = (uint32_t)c * 2u;
+  const uint32_t wbase = Fmt<FMT>::woff(q, c);
+  const int p = blockIdx.x;
+  const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
+  const NibConst k = nib_const();
+  Best bs;
+  best_init(bs);
+
+  // this wave's first item in unit u2 or later (u2 = u1: none)
+  auto first_from = [&](int& u2, int& g2) {
+    g2 = wave;
+    if (wave >= a.G) u2 = u1;
+  };
+  auto advance = [&](int& u2, int& g2) {
+    g2 += W;
+    if (g2 >= a.G) {
+      ++u2;
+      g2 = wave;
+    }
+  };
+  auto load_item = [&](RowsData<FMT, S, XL>& d, int u2, int g2) {
+    const int b = u2 / kPer, st0 = (u2 % kPer) * S;
+    rows_load<FMT, S, XL>(d, rs, (uint32_t)b * (uint32_t)a.G + (uint32_t)g2, g2,
+                          wbase + (uint32_t)st0 * kQuad, (uint32_t)(4 * c + st0) * 2u, zoff,
+                          xoff);
+  };
+
+  RowsData<FMT, S, XL> buf[D];
+  int cu[D], cg[D];
+  int lu = u0, lg = 0;
+  first_from(lu, lg);
+  const u32x4* xrow = xlds + ((c < a.M ? c : a.M - 1) * a.K + 32 * q) / 8;
+  auto prime = [&]() {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      cu[j] = lu;
+      cg[j] = lg;
+      if (lu < u1) {
+        load_item(buf[j], lu, lg);
+        advance(lu, lg);
+      }
+    }
+  };
+  if (XL) {
+    // x loads first, then the first weight items: waiting for x leaves the
+    // weights in flight (loads complete in order)
+    const int n16 = a.M * a.K / 8;
+    u32x4 xv[kRowsXChunks];
+#pragma unroll
+    for (int j = 0; j < kRowsXChunks; ++j) {
+      const int i = threadIdx.x + j * 64 * W;
+      if (i < n16) xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)i * 16u, 0, 0);
+    }
+    prime();
+#pragma unroll
+    for (int j = 0; j < kRowsXChunks; ++j) {
+      const int i = threadIdx.x + j * 64 * W;
+      if (i < n16) xlds[i] = xv[j];
+    }
+    __syncthreads();
+  } else {
+    prime();
+  }
+
+  f32x4 acc[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int par = 0, closed = u0;
+  auto close_unit = [&]() {
+#pragma unroll
+    for (int i = 0; i < S; ++i) red[par][wave][i][lane] = acc[i];
+    __syncthreads();
+    if (wave == 0) {
+      f32x4 t[S];
+#pragma unroll
+      for (int i = 0; i < S; ++i) t[i] = red[par][0][i][lane];
+      for (int w = 1; w < W; ++w)
+#pragma unroll
+        for (int i = 0; i < S; ++i) t[i] += red[par][w][i][lane];
+      emit_rows<OUT, S>(a, closed / kPer, (closed % kPer) * S, t, lane, bs);
+    }
+    par ^= 1;
+    ++closed;
+#pragma unroll
+    for (int i = 0; i < S; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  };
+
+  while (cu[0] < u1) {
+    RowsData<FMT, S, XL> nw;
+    const int nu = lu, ng = lg;
+    if (lu < u1) {
+      load_item(nw, lu, lg);
+      advance(lu, lg);
+    }
+    while (closed < cu[0]) close_unit();
+    rows_mma<FMT, S, XL>(acc, buf[0], k, (cu[0] % kPer) * S, xrow + cg[0] * 16);
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j) {
+      buf[j] = buf[j + 1];
+      cu[j] = cu[j + 1];
+      cg[j] = cg[j + 1];
+    }
+    buf[D - 1] = nw;
+    cu[D - 1] = nu;
+    cg[D - 1] = ng;
+  }
+  while (closed < u1) close_unit();
+  if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
+}
+
 // ------------------------------------------------------------- host side
 // Workgroups per CU: the kernel's occupancy (all workgroups resident in one
 // round, equal work each). QW4_SKINNY_WGS_PER_CU, QW4_SKINNY_W (4|8|16) and
@@ -643,14 +894,70 @@ int wgs_per_cu() {
 
 struct Launch {
   int W, P;
+  int S;    // 0: stream-K (k_skinny); 1, 2, 4: k_rows with units of S row quads
+  bool XL;  // k_rows: activations staged in LDS
 };
+
+// Items each k_rows wave keeps in flight, by unit size.
+template <int S, bool XL>
+constexpr int rows_depth() {
+  return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 2)) : (S == 4 ? 1 : 2);
+}
+
+// Workgroups per CU of k_rows without dynamic LDS (registers, waves and static
+// LDS), cached per device; the caller applies the staged activations' LDS.
+template <int OUT, int FMT, int S, int W>
+int rows_wgs_per_cu(bool xl) {
+  static int slot[64][2] = {{0}};
+  int& v = slot[current_device()][xl ? 1 : 0];
+  if (!v) {
+    int n = 0;
+    hipError_t e = xl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                            &n, k_rows<OUT, FMT, S, W, true, rows_depth<S, true>()>, 64 * W, 0)
+                      : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                            &n, k_rows<OUT, FMT, S, W, false, rows_depth<S, false>()>, 64 * W, 0);
+    if (e != hipSuccess || n <= 0) n = 1;
+    v = std::min(n, kMaxWgsPerCu);
+  }
+  return v;
+}
+
+// Static LDS of the staged-activation kernel (hipFuncGetAttributes).
+template <int OUT, int FMT, int S, int W>
+int rows_static_lds_s() {
+  static int slot[64] = {0};
+  int& v = slot[current_device()];
+  if (!v) {
+    hipFuncAttributes at{};
+    v = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(
+                                      k_rows<OUT, FMT, S, W, true, rows_depth<S, true>()>)) ==
+                hipSuccess
+            ? (int)at.sharedSizeBytes
+            : kLdsBytes;   // unknown: never stage
+  }
+  return v;
+}
+
+template <int OUT, int FMT, int W>
+int rows_static_lds(int S) {
+  return S == 4   ? rows_static_lds_s<OUT, FMT, 4, W>()
+         : S == 2 ? rows_static_lds_s<OUT, FMT, 2, W>()
+                  : rows_static_lds_s<OUT, FMT, 1, W>();
+}
+
+template <int OUT, int FMT, int W>
+int rows_occ(int S, bool xl) {
+  return S == 4   ? rows_wgs_per_cu<OUT, FMT, 4, W>(xl)
+         : S == 2 ? rows_wgs_per_cu<OUT, FMT, 2, W>(xl)
+                  : rows_wgs_per_cu<OUT, FMT, 1, W>(xl);
+}
 
 // Default: W = 4 stream-K over every resident slot. Small outputs with short K
 // (measured on MI355X: the 19 MB qkv and 11 MB o projections) do better with
 // more waves per tile and fewer split tiles: M = 1 uses W = 16 with two
 // workgroups per tile, M > 1 W = 8 with one.
 template <int OUT, bool M1, int FMT = 4>
-Launch launch_for(int out_f, int G) {
+Launch launch_for(int out_f, int G, int M) {
   read_env();
   const int tiles = out_f / kTileN;
   const long long U = (long long)tiles * G;
@@ -672,7 +979,59 @@ Launch launch_for(int out_f, int G) {
   // at most 64 workgroups may share a tile: keep ranges >= G / 60 blocks
   cap = std::min(cap, std::max<long long>(1, U * 60 / G));
   l.P = (int)std::max<long long>(1, std::min(cap, (U + l.W - 1) / l.W));
+  l.S = 0;
+  // Data-parallel k_rows (no cross-workgroup exchange) by default. Unit size
+  // and waves measured on MI355X over the model's projections and the head:
+  // S = 2 (32-row units) when the output has fewer 64-row tiles than CUs,
+  // else S = 4; M = 1: 16 waves for K >= 64 groups, else 8; M > 1: 16 waves
+  // with S = 2, 8 with S = 4. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces
+  // S (read on every call); QW4_ROWS_W forces the waves.
+  const char* er = std::getenv("QW4_ROWS");
+  const int env_rows = er ? std::atoi(er) : -1;
+  const char* ew = std::getenv("QW4_ROWS_W");
+  const int env_rows_w = ew ? std::atoi(ew) : 0;
+  l.XL = false;
+  if (env_rows == 0) return l;
+  l.S = (env_rows == 1 || env_rows == 2 || env_rows == 4) ? env_rows
+                                                          : (tiles < device_cus() ? 2 : 4);
+  if (env_rows_w == 8 || env_rows_w == 16)
+    l.W = env_rows_w;
+  else if (M == 1)
+    l.W = G >= 64 ? 16 : 8;
+  else
+    l.W = l.S == 2 ? 16 : 8;
+  const int xbytes = M * G * kGroup * 2;
+  // the kernel's static LDS + the activations within the CU's LDS
+  const int static_lds =
+      l.W == 8 ? rows_static_lds<OUT, FMT, 8>(l.S) : rows_static_lds<OUT, FMT, 16>(l.S);
+  l.XL = xbytes <= kRowsXChunks * 16 * 64 * l.W && static_lds + xbytes <= kLdsBytes;
+  const long long units = (long long)tiles * 4 / l.S;
+  int occ = l.W == 8 ? rows_occ<OUT, FMT, 8>(l.S, l.XL) : rows_occ<OUT, FMT, 16>(l.S, l.XL);
+  if (l.XL) occ = std::max(1, std::min(occ, kLdsBytes / (static_lds + xbytes)));
+  long long pc = (long long)device_cus() * occ;
+  if (env_p > 0) pc = env_p;
+  l.P = (int)std::max<long long>(1, std::min(units, pc));
   return l;
+}
+
+template <int OUT, int FMT, int W, bool XL>
+void launch_rows_x(const SkinnyArgs& a, int S, hipStream_t st) {
+  const size_t lds = XL ? (size_t)a.M * a.K * 2 : 0;
+  if (S == 4)
+    k_rows<OUT, FMT, 4, W, XL, rows_depth<4, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+  else if (S == 2)
+    k_rows<OUT, FMT, 2, W, XL, rows_depth<2, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+  else
+    k_rows<OUT, FMT, 1, W, XL, rows_depth<1, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+}
+
+template <int OUT, int FMT>
+void launch_rows(const SkinnyArgs& a, int S, int W, bool xl, hipStream_t st) {
+  if (W == 8)
+    xl ? launch_rows_x<OUT, FMT, 8, true>(a, S, st) : launch_rows_x<OUT, FMT, 8, false>(a, S, st);
+  else
+    xl ? launch_rows_x<OUT, FMT, 16, true>(a, S, st)
+       : launch_rows_x<OUT, FMT, 16, false>(a, S, st);
 }
 
 template <int OUT, bool M1, int FMT>
@@ -710,8 +1069,8 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   // loads address weights and x through 32-bit buffer offsets
   if (w.weight_bytes >= (1ull << 32)) return QW4_ERR_SHAPE;
   const bool m1 = M == 1;
-  const Launch l = m1 ? launch_for<OUT, true, FMT>(w.out_f, w.G)
-                      : launch_for<OUT, false, FMT>(w.out_f, w.G);
+  const Launch l = m1 ? launch_for<OUT, true, FMT>(w.out_f, w.G, M)
+                      : launch_for<OUT, false, FMT>(w.out_f, w.G, M);
   if ((size_t)l.P * 2 * 1024 > slot_floats() ||
       slot_floats() + (size_t)tiles * 64 * 2 > s->partial_elems)
     return QW4_ERR_SCRATCH;
@@ -735,6 +1094,12 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.U = tiles * w.G;
   a.slot_bytes = (uint32_t)(slot_floats() * 4);
   a.weight_bytes = (uint32_t)w.weight_bytes;
+  if (l.S) {
+    a.U = tiles * 4 / l.S;
+    launch_rows<OUT, FMT>(a, l.S, l.W, l.XL, (hipStream_t)stream);
+    QW4_LAUNCH_CHECK();
+    return QW4_OK;
+  }
   if (m1)
     launch<OUT, true, FMT>(a, l.W, (hipStream_t)stream);
   else
@@ -782,7 +1147,9 @@ extern "C" {
 int qw4_choose_splits(int out_f, int num_groups) {
   if (out_f < kTileN || num_groups <= 0) return 1;
   const long long U = (long long)(out_f / kTileN) * num_groups;
-  const long long P = launch_for<OUT_BF16, true>(out_f, num_groups).P;
+  const Launch l = launch_for<OUT_BF16, true>(out_f, num_groups, 1);
+  if (l.S) return 1;   // whole units per workgroup: no split
+  const long long P = l.P;
   // workgroups sharing one tile, at most: ceil(G / blocks-per-workgroup) + 1
   const long long per = std::max<long long>(1, U / P);
   return (int)std::min<long long>(P, (num_groups + per - 1) / per + (U % P ? 1 : 0));

@@ -19,3 +19,15 @@ def orc():
     import oracle
 
     return oracle
+
+
+@pytest.fixture(params=["rows", "streamk"])
+def decode_path(request, monkeypatch):
+    """Runs a decode/verify test through both skinny kernels: the default
+    data-parallel k_rows and the stream-K kernel (QW4_ROWS=0, read by the
+    library on every call)."""
+    if request.param == "streamk":
+        monkeypatch.setenv("QW4_ROWS", "0")
+    else:
+        monkeypatch.delenv("QW4_ROWS", raising=False)
+    return request.param

@@ -134,7 +134,7 @@ def _run_gemv(hip, orc, scratch, N, K, seed, M=1, f32=False):
     return w, dx, y, ref
 
 
-def test_gemv_config1(hip, orc, scratch):
+def test_gemv_config1(hip, orc, scratch, decode_path):
     """M=1, K=N=5120, seed 0."""
     import torch
 
@@ -162,7 +162,7 @@ def test_gemv_config1(hip, orc, scratch):
                                  # rows (N / 8), o and down by columns (K / 8), lm_head
                                  (896, 5120), (4352, 5120), (5120, 512), (5120, 2176),
                                  (31040, 5120), (64, 640)])
-def test_gemv_layer_shapes(hip, orc, scratch, N, K):
+def test_gemv_layer_shapes(hip, orc, scratch, decode_path, N, K):
     w, _, y, ref = _run_gemv(hip, orc, scratch, N, K, seed=N + K)
     _check_bf16(orc, host(y, np.uint16), ref, f"gemv {N}x{K}")
     hip.awq_free(w)
@@ -170,7 +170,7 @@ def test_gemv_layer_shapes(hip, orc, scratch, N, K):
 
 @pytest.mark.parametrize("M", [2, 9, 12, 16])
 @pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 17408), (128, 1024), (5120, 2176)])
-def test_verify_skinny(hip, orc, scratch, M, N, K):
+def test_verify_skinny(hip, orc, scratch, decode_path, M, N, K):
     """speculative-verify M in {9, 12, 16} (and M=2)."""
     w, _, y, ref = _run_gemv(hip, orc, scratch, N, K, seed=3 * M + N, M=M)
     _check_bf16(orc, host(y, np.uint16), ref, f"verify M={M} {N}x{K}")
@@ -194,7 +194,7 @@ def test_mma_entry_matches_small(hip, orc, scratch):
 
 # ------------------------------------------------------- lm_head + argmax
 @pytest.mark.parametrize("N,M", [(4096, 1), (4096, 9), (248320, 1), (248320, 9)])
-def test_lm_head_argmax(hip, orc, scratch, N, M):
+def test_lm_head_argmax(hip, orc, scratch, decode_path, N, M):
     """INT4 lm_head GEMV + fused fp32 row-argmax, exact indices."""
     import torch
 

@@ -151,7 +151,7 @@ def _run(hip, orc, scratch, N, K, M, seed):
 
 @pytest.mark.parametrize("M", [1, 2, 9, 16])
 @pytest.mark.parametrize("N,K", [(64, 512), (5120, 5120), (31040, 5120), (640, 2176)])
-def test_w8_gemv_and_verify(hip, orc, scratch, N, K, M):
+def test_w8_gemv_and_verify(hip, orc, scratch, decode_path, N, K, M):
     import torch
 
     w, dx, y, ref = _run(hip, orc, scratch, N, K, M, seed=N + M)
@@ -171,7 +171,7 @@ def test_w8_gemv_and_verify(hip, orc, scratch, N, K, M):
 
 
 @pytest.mark.parametrize("M", [1, 9])
-def test_w8_lm_head_argmax_full_vocab(hip, orc, scratch, M):
+def test_w8_lm_head_argmax_full_vocab(hip, orc, scratch, decode_path, M):
     """The reference's default head (lm_head_bits 8, model.cu:796-815, :1044-1047)
     at the full vocabulary: quantize 248320 x 5120 on the GPU (bytes and scales
     bit-exact against the oracle), then the fused GEMV + fp32 row-argmax."""
