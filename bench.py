@@ -433,8 +433,8 @@ def main():
                      "achieved": round(d["avg_bytes"] / (d["avg_ms"] * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["avg_bytes"] / (d["avg_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("k_skinny_decode_sweep"),
-                     "kernel": "k_skinny (decode GEMV), avg over the sweep's 4 shapes",
+                     "traffic": traffic_from_profiles("k_rows_decode_sweep"),
+                     "kernel": "k_rows (decode GEMV), avg over the sweep's 4 shapes",
                      "alg_bytes_per_launch": round(d["avg_bytes"]),
                      "avg_launch_us": round(d["avg_ms"] * 1e3, 3)},
         "cpu_baseline": cpu,

@@ -274,7 +274,6 @@ struct Fmt;
 template <>
 struct Fmt<4> {
   using Data = GroupData;
-  static constexpr uint32_t kBlockBytes = 4096;
   __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 1024 + c * 16); }
   __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
                               int c, uint32_t woff, uint32_t xoff) {
@@ -285,7 +284,6 @@ struct Fmt<4> {
 template <>
 struct Fmt<8> {
   using Data = GroupData8;
-  static constexpr uint32_t kBlockBytes = 8192;
   __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 2048 + c * 32); }
   __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
                               int c, uint32_t woff, uint32_t xoff) {
