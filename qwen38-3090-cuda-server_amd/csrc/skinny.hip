@@ -57,6 +57,9 @@
 #include "w4a16_common.h"
 
 namespace qw4 {
+// Cache policy of the decode kernels' weight loads: nontemporal (each byte is
+// read once per call; measured 3-6% faster than the default policy).
+constexpr int kWeightAux = 2;
 int check_weights_public(const qw4_weights* w);
 
 namespace {
@@ -615,7 +618,7 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
 #pragma unroll
     for (int h = 0; h < (FMT == 8 ? 2 : 1); ++h)
       d.w[i][h] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + i * kQuad + h * 16,
-                                                        blk * kBlk, 0);
+                                                        blk * kBlk, kWeightAux);
   if (!XL) {
 #pragma unroll
     for (int t = 0; t < 4; ++t)
@@ -629,22 +632,40 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
   } else if (S == 2) {
     d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff, blk * 128u, 0);
   } else {
-    d.s[0] = __builtin_amdgcn_raw_buffer_load_b16(r.sc, soff, blk * 128u, 0);
+    // the aligned word holding this row's scale (half st0 & 1)
+    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff & ~3u, blk * 128u, 0);
   }
-  if (FMT == 4) d.z = __builtin_amdgcn_raw_buffer_load_b16(r.zr, zoff, blk * 32u, 0);
+  // 32-bit loads only: a 16-bit load result gets masked right after the load,
+  // which makes the compiler wait for it there (zoff: the aligned word holding
+  // this lane's 16 bits)
+  if (FMT == 4) d.z = __builtin_amdgcn_raw_buffer_load_b32(r.zr, zoff, blk * 32u, 0);
 }
 
 // XL: activations come from LDS (xl: this lane's row, k chunk q, group g);
 // otherwise from the registers rows_load filled.
 template <int FMT, int S, bool XL>
 __device__ __forceinline__ void rows_mma(f32x4 (&acc)[S], const RowsData<FMT, S, XL>& d, NibConst k,
-                                         int st0, const u32x4* xl) {
+                                         int st0, int zsh, const u32x4* xl) {
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
                                                        0x3F803F80u, 0x3F803F80u});
   f32x4 C[S], Cs;
   u32x4 xr[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) xr[t] = XL ? xl[t] : d.x[t & (XL ? 0 : 3)];
+  // Scale and zero point first, pinned here: the loaded words must be dead
+  // before the caller reloads this buffer, or the compiler keeps both copies
+  // and moves them at the loop's back edge (waiting for the newest loads).
+  float sf[S], zf[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const uint32_t sbits = (d.s[i >> 1] >> (16 * (S == 1 ? (st0 & 1) : (i & 1)))) & 0xffffu;
+    sf[i] = bf16_bits_to_f32(sbits);
+    zf[i] = FMT == 4 ? 128.0f + (float)((d.z >> (zsh + 4 * (st0 + i))) & 0xFu) : 128.0f;
+    // staged activations (M = 1): pinned here, so the loaded words are dead
+    // before the caller reloads the buffer (measured 1% faster; with
+    // activations in registers the extra live values would spill)
+    if (XL) asm volatile("" : "+v"(sf[i]), "+v"(zf[i])::"memory");
+  }
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const bf16x8 A = __builtin_bit_cast(bf16x8, xr[t]);
@@ -665,13 +686,9 @@ __device__ __forceinline__ void rows_mma(f32x4 (&acc)[S], const RowsData<FMT, S,
                                                  0, 0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < S; ++i) {
-    const uint32_t sbits = (d.s[i >> 1] >> (16 * (i & 1))) & 0xffffu;
-    const float sf = bf16_bits_to_f32(sbits);
-    const float zf = FMT == 4 ? 128.0f + (float)((d.z >> (4 * (st0 + i))) & 0xFu) : 128.0f;
+  for (int i = 0; i < S; ++i)
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) acc[i][jj] += sf * (C[i][jj] - zf * Cs[jj]);
-  }
+    for (int jj = 0; jj < 4; ++jj) acc[i][jj] += sf[i] * (C[i][jj] - zf[i] * Cs[jj]);
 }
 
 // Final values of one unit (wave 0): rows m = 4q + jj, columns b*64 + 4c + st0 + i.
@@ -706,13 +723,18 @@ __device__ __forceinline__ void emit_rows(const SkinnyArgs& a, int b, int st0,
   }
 }
 
-// Each wave walks its items (unit u, group g), g = wave, wave + W, ... < G,
-// over the workgroup's units [start(p), start(p + 1)) in order, D items ahead
-// (the next loads are issued across unit boundaries too). Every wave closes
-// every unit: it writes its partial (zero if it had no item) to one of two LDS
-// buffers and passes one barrier, so the waves stay in step for any G; wave 0
-// then sums the W partials in wave order and emits the unit. No workgroup
-// depends on another.
+// k_rows: workgroup p owns the whole units [start(p), start(p + 1)). Each
+// wave walks its items (unit u, group g), g = wave, wave + W, ... < G, over
+// those units in order, D items ahead of the math (the next loads are issued
+// across unit boundaries too). Buffer j holds items j, j + D, ...: the loop is
+// unrolled by D, so no buffer is ever copied (a register copy would have to
+// wait for its load and drain the pipeline every item), and every item issues
+// the same loads -- past the end they are out of range and return zeros with
+// no traffic -- so the wait counts are static. Every wave closes every unit:
+// it writes its partial (zero if it had no item) to one of two LDS buffers
+// and passes one barrier, so the waves stay in step for any G; wave 0 then
+// sums the W partials in wave order and emits the unit. No workgroup depends
+// on another.
 template <int OUT, int FMT, int S, int W, bool XL, int D>
 __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   constexpr int kPer = 4 / S;   // units per tile
@@ -724,7 +746,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   const int c = lane & 15, q = lane >> 4;
   const SkinnyRsrc rs = skinny_rsrc(a);
   const uint32_t xoff = (uint32_t)(c * a.K + 32 * q) * 2u;
-  const uint32_t zoff = (uint32_t)c * 2u;
+  const uint32_t zoff = (uint32_t)(c & ~1) * 2u;   // word with this lane's zero points
+  const int zsh = 16 * (c & 1);
   const uint32_t wbase = Fmt<FMT>::woff(q, c);
   const int p = blockIdx.x;
   const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
@@ -732,57 +755,48 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   Best bs;
   best_init(bs);
 
-  // this wave's first item in unit u2 or later (u2 = u1: none)
-  auto first_from = [&](int& u2, int& g2) {
-    g2 = wave;
-    if (wave >= a.G) u2 = u1;
-  };
-  auto advance = [&](int& u2, int& g2) {
-    g2 += W;
-    if (g2 >= a.G) {
-      ++u2;
-      g2 = wave;
-    }
-  };
-  auto load_item = [&](RowsData<FMT, S, XL>& d, int u2, int g2) {
-    const int b = u2 / kPer, st0 = (u2 % kPer) * S;
-    rows_load<FMT, S, XL>(d, rs, (uint32_t)b * (uint32_t)a.G + (uint32_t)g2, g2,
+  const int nw = wave < a.G ? (a.G - 1 - wave) / W + 1 : 0;   // items per unit
+  const int T = nw * (u1 - u0);
+  const uint32_t oob_blk = (uint32_t)a.tiles * (uint32_t)a.G;
+  int lu = u0, lg = wave;   // load cursor (wave-uniform)
+  auto load_next = [&](RowsData<FMT, S, XL>& d) {
+    const bool in = lu < u1;
+    const int b = in ? lu / kPer : 0, st0 = in ? (lu % kPer) * S : 0;
+    const int g = in ? lg : 0;
+    rows_load<FMT, S, XL>(d, rs, in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk, g,
                           wbase + (uint32_t)st0 * kQuad, (uint32_t)(4 * c + st0) * 2u, zoff,
                           xoff);
+    lg += W;
+    if (lg >= a.G) {
+      lg = wave;
+      ++lu;
+    }
   };
 
   RowsData<FMT, S, XL> buf[D];
-  int cu[D], cg[D];
-  int lu = u0, lg = 0;
-  first_from(lu, lg);
   const u32x4* xrow = xlds + ((c < a.M ? c : a.M - 1) * a.K + 32 * q) / 8;
   auto prime = [&]() {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      cu[j] = lu;
-      cg[j] = lg;
-      if (lu < u1) {
-        load_item(buf[j], lu, lg);
-        advance(lu, lg);
-      }
-    }
+    for (int j = 0; j < D; ++j) load_next(buf[j]);
   };
   if (XL) {
     // x loads first, then the first weight items: waiting for x leaves the
-    // weights in flight (loads complete in order)
+    // weights in flight (loads complete in order). Threads past the last
+    // chunk repeat it (same address, same value), so neither the loads nor
+    // the LDS stores are conditional and the scheduler cannot sink the loads
+    // behind the weights.
     const int n16 = a.M * a.K / 8;
     u32x4 xv[kRowsXChunks];
+    int xi[kRowsXChunks];
 #pragma unroll
     for (int j = 0; j < kRowsXChunks; ++j) {
-      const int i = threadIdx.x + j * 64 * W;
-      if (i < n16) xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)i * 16u, 0, 0);
+      xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
+      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
     }
+    __builtin_amdgcn_sched_barrier(0);
     prime();
 #pragma unroll
-    for (int j = 0; j < kRowsXChunks; ++j) {
-      const int i = threadIdx.x + j * 64 * W;
-      if (i < n16) xlds[i] = xv[j];
-    }
+    for (int j = 0; j < kRowsXChunks; ++j) xlds[xi[j]] = xv[j];
     __syncthreads();
   } else {
     prime();
@@ -811,26 +825,28 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     for (int i = 0; i < S; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   };
 
-  while (cu[0] < u1) {
-    RowsData<FMT, S, XL> nw;
-    const int nu = lu, ng = lg;
-    if (lu < u1) {
-      load_item(nw, lu, lg);
-      advance(lu, lg);
+  int cg = wave;   // compute cursor: unit `closed`, group cg
+  auto step = [&](RowsData<FMT, S, XL>& d, bool reload) {
+    rows_mma<FMT, S, XL>(acc, d, k, (closed % kPer) * S, zsh, xrow + cg * 16);
+    if (reload) load_next(d);
+    cg += W;
+    if (cg >= a.G) {
+      cg = wave;
+      close_unit();
     }
-    while (closed < cu[0]) close_unit();
-    rows_mma<FMT, S, XL>(acc, buf[0], k, (cu[0] % kPer) * S, xrow + cg[0] * 16);
+  };
+  // whole rounds of D items with no conditional loads (a conditional load
+  // would make the compiler's wait counts assume the shortest path), then
+  // the last < D items, already loaded
+  int t0 = 0;
+  for (; t0 + D <= T; t0 += D) {
 #pragma unroll
-    for (int j = 0; j < D - 1; ++j) {
-      buf[j] = buf[j + 1];
-      cu[j] = cu[j + 1];
-      cg[j] = cg[j + 1];
-    }
-    buf[D - 1] = nw;
-    cu[D - 1] = nu;
-    cg[D - 1] = ng;
+    for (int j = 0; j < D; ++j) step(buf[j], true);
   }
-  while (closed < u1) close_unit();
+#pragma unroll
+  for (int j = 0; j < D - 1; ++j)
+    if (t0 + j < T) step(buf[j], false);
+  while (closed < u1) close_unit();   // waves with no items (wave >= G)
   if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
 }
 
@@ -896,10 +912,23 @@ struct Launch {
   bool XL;  // k_rows: activations staged in LDS
 };
 
-// Items each k_rows wave keeps in flight, by unit size.
-template <int S, bool XL>
+// Items each k_rows wave keeps in flight (the one being computed included),
+// by output, weight format, unit size, activation source and waves: as deep
+// as fits the registers without spilling (16 waves: 128 VGPRs; 8 waves: 256).
+// The argmax runs with 8 waves only.
+template <int OUT, int FMT, int S, bool XL, int W>
 constexpr int rows_depth() {
-  return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 2)) : (S == 4 ? 1 : 2);
+  if (FMT == 8) {
+    if (OUT == OUT_ARGMAX) return XL ? (S == 1 ? 4 : (S == 2 ? 2 : 1)) : 1;
+    if (W == 16) return XL ? (S == 1 ? 3 : 1) : 1;
+    return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 2)) : (S == 4 ? 1 : 2);
+  }
+  if (OUT == OUT_ARGMAX) {
+    if (W == 16) return 1;
+    return XL ? (S == 1 ? 5 : (S == 2 ? 3 : 2)) : (S == 4 ? 1 : 2);
+  }
+  if (W == 16) return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 1)) : 1;
+  return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 2)) : (S == 4 ? 2 : 3);
 }
 
 // Workgroups per CU of k_rows without dynamic LDS (registers, waves and static
@@ -911,9 +940,9 @@ int rows_wgs_per_cu(bool xl) {
   if (!v) {
     int n = 0;
     hipError_t e = xl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                            &n, k_rows<OUT, FMT, S, W, true, rows_depth<S, true>()>, 64 * W, 0)
+                            &n, k_rows<OUT, FMT, S, W, true, rows_depth<OUT, FMT, S, true, W>()>, 64 * W, 0)
                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                            &n, k_rows<OUT, FMT, S, W, false, rows_depth<S, false>()>, 64 * W, 0);
+                            &n, k_rows<OUT, FMT, S, W, false, rows_depth<OUT, FMT, S, false, W>()>, 64 * W, 0);
     if (e != hipSuccess || n <= 0) n = 1;
     v = std::min(n, kMaxWgsPerCu);
   }
@@ -928,7 +957,7 @@ int rows_static_lds_s() {
   if (!v) {
     hipFuncAttributes at{};
     v = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(
-                                      k_rows<OUT, FMT, S, W, true, rows_depth<S, true>()>)) ==
+                                      k_rows<OUT, FMT, S, W, true, rows_depth<OUT, FMT, S, true, W>()>)) ==
                 hipSuccess
             ? (int)at.sharedSizeBytes
             : kLdsBytes;   // unknown: never stage
@@ -969,10 +998,9 @@ Launch launch_for(int out_f, int G, int M) {
   else
     cap = (long long)tiles * (l.W == 16 ? 2 : 1);
   if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
-  static const int env_p = [] {
-    const char* e = std::getenv("QW4_SKINNY_P");
-    return e ? std::atoi(e) : 0;
-  }();
+  // read on every call (tuning only)
+  const char* ep = std::getenv("QW4_SKINNY_P");
+  const int env_p = ep ? std::atoi(ep) : 0;
   if (env_p > 0) cap = env_p;
   // at most 64 workgroups may share a tile: keep ranges >= G / 60 blocks
   cap = std::min(cap, std::max<long long>(1, U * 60 / G));
@@ -981,9 +1009,9 @@ Launch launch_for(int out_f, int G, int M) {
   // Data-parallel k_rows (no cross-workgroup exchange) by default. Unit size
   // and waves measured on MI355X over the model's projections and the head:
   // S = 2 (32-row units) when the output has fewer 64-row tiles than CUs,
-  // else S = 4; M = 1: 16 waves for K >= 64 groups, else 8; M > 1: 16 waves
-  // with S = 2, 8 with S = 4. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces
-  // S (read on every call); QW4_ROWS_W forces the waves.
+  // else S = 4; M = 1: 16 waves for K >= 64 groups, else 8; M > 1 and the
+  // argmax: 8 waves. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces S (read
+  // on every call); QW4_ROWS_W forces the waves.
   const char* er = std::getenv("QW4_ROWS");
   const int env_rows = er ? std::atoi(er) : -1;
   const char* ew = std::getenv("QW4_ROWS_W");
@@ -992,19 +1020,28 @@ Launch launch_for(int out_f, int G, int M) {
   if (env_rows == 0) return l;
   l.S = (env_rows == 1 || env_rows == 2 || env_rows == 4) ? env_rows
                                                           : (tiles < device_cus() ? 2 : 4);
-  if (env_rows_w == 8 || env_rows_w == 16)
+  if (OUT == OUT_ARGMAX)
+    l.W = 8;   // the running argmax does not fit 16 waves' registers
+  else if (env_rows_w == 8 || env_rows_w == 16)
     l.W = env_rows_w;
   else if (M == 1)
     l.W = G >= 64 ? 16 : 8;
   else
-    l.W = l.S == 2 ? 16 : 8;
+    l.W = 8;
   const int xbytes = M * G * kGroup * 2;
   // the kernel's static LDS + the activations within the CU's LDS
-  const int static_lds =
-      l.W == 8 ? rows_static_lds<OUT, FMT, 8>(l.S) : rows_static_lds<OUT, FMT, 16>(l.S);
+  int static_lds = 0;
+  if constexpr (OUT == OUT_ARGMAX)
+    static_lds = rows_static_lds<OUT, FMT, 8>(l.S);
+  else
+    static_lds = l.W == 8 ? rows_static_lds<OUT, FMT, 8>(l.S) : rows_static_lds<OUT, FMT, 16>(l.S);
   l.XL = xbytes <= kRowsXChunks * 16 * 64 * l.W && static_lds + xbytes <= kLdsBytes;
   const long long units = (long long)tiles * 4 / l.S;
-  int occ = l.W == 8 ? rows_occ<OUT, FMT, 8>(l.S, l.XL) : rows_occ<OUT, FMT, 16>(l.S, l.XL);
+  int occ = 1;
+  if constexpr (OUT == OUT_ARGMAX)
+    occ = rows_occ<OUT, FMT, 8>(l.S, l.XL);
+  else
+    occ = l.W == 8 ? rows_occ<OUT, FMT, 8>(l.S, l.XL) : rows_occ<OUT, FMT, 16>(l.S, l.XL);
   if (l.XL) occ = std::max(1, std::min(occ, kLdsBytes / (static_lds + xbytes)));
   long long pc = (long long)device_cus() * occ;
   if (env_p > 0) pc = env_p;
@@ -1016,20 +1053,21 @@ template <int OUT, int FMT, int W, bool XL>
 void launch_rows_x(const SkinnyArgs& a, int S, hipStream_t st) {
   const size_t lds = XL ? (size_t)a.M * a.K * 2 : 0;
   if (S == 4)
-    k_rows<OUT, FMT, 4, W, XL, rows_depth<4, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+    k_rows<OUT, FMT, 4, W, XL, rows_depth<OUT, FMT, 4, XL, W>()><<<a.P, 64 * W, lds, st>>>(a);
   else if (S == 2)
-    k_rows<OUT, FMT, 2, W, XL, rows_depth<2, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+    k_rows<OUT, FMT, 2, W, XL, rows_depth<OUT, FMT, 2, XL, W>()><<<a.P, 64 * W, lds, st>>>(a);
   else
-    k_rows<OUT, FMT, 1, W, XL, rows_depth<1, XL>()><<<a.P, 64 * W, lds, st>>>(a);
+    k_rows<OUT, FMT, 1, W, XL, rows_depth<OUT, FMT, 1, XL, W>()><<<a.P, 64 * W, lds, st>>>(a);
 }
 
 template <int OUT, int FMT>
-void launch_rows(const SkinnyArgs& a, int S, int W, bool xl, hipStream_t st) {
-  if (W == 8)
-    xl ? launch_rows_x<OUT, FMT, 8, true>(a, S, st) : launch_rows_x<OUT, FMT, 8, false>(a, S, st);
+void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
+  if (OUT == OUT_ARGMAX || l.W == 8)
+    l.XL ? launch_rows_x<OUT, FMT, 8, true>(a, l.S, st) : launch_rows_x<OUT, FMT, 8, false>(a, l.S, st);
   else
-    xl ? launch_rows_x<OUT, FMT, 16, true>(a, S, st)
-       : launch_rows_x<OUT, FMT, 16, false>(a, S, st);
+    if constexpr (OUT != OUT_ARGMAX)
+      l.XL ? launch_rows_x<OUT, FMT, 16, true>(a, l.S, st)
+           : launch_rows_x<OUT, FMT, 16, false>(a, l.S, st);
 }
 
 template <int OUT, bool M1, int FMT>
@@ -1094,7 +1132,7 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.weight_bytes = (uint32_t)w.weight_bytes;
   if (l.S) {
     a.U = tiles * 4 / l.S;
-    launch_rows<OUT, FMT>(a, l.S, l.W, l.XL, (hipStream_t)stream);
+    launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
     QW4_LAUNCH_CHECK();
     return QW4_OK;
   }

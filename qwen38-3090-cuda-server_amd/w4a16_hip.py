@@ -15,7 +15,7 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqwen_w4a16.so")
+LIB_PATH = os.environ.get("QW4_LIB") or os.path.join(HERE, "libqwen_w4a16.so")
 
 QW4_OK = 0
 QW4_ERR_NULL = 1

@@ -161,7 +161,9 @@ def test_gemv_config1(hip, orc, scratch, decode_path):
                                  # one GPU's shard of an 8-way split: qkv and gate|up by
                                  # rows (N / 8), o and down by columns (K / 8), lm_head
                                  (896, 5120), (4352, 5120), (5120, 512), (5120, 2176),
-                                 (31040, 5120), (64, 640)])
+                                 (31040, 5120), (64, 640),
+                                 # one group (waves past G idle) and an odd group count
+                                 (64, 128), (192, 384)])
 def test_gemv_layer_shapes(hip, orc, scratch, decode_path, N, K):
     w, _, y, ref = _run_gemv(hip, orc, scratch, N, K, seed=N + K)
     _check_bf16(orc, host(y, np.uint16), ref, f"gemv {N}x{K}")
