@@ -170,6 +170,54 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M,
 int qw4_argmax(int32_t* out, const uint16_t* x, int n, int32_t* scratch, void* stream);
 int qw4_argmax_rows(int32_t* out, const uint16_t* x, int rows, int n, void* stream);
 
+/* ------------------------------------------------- layer steps either side
+ * The elementwise steps around the projections in the reference's layer
+ * (src/kernels/elementwise.cuh:8-22, .cu:8-49; called at
+ * src/model/model.cu:697, :772-785). Data bf16, 16-byte aligned.
+ *
+ * rmsnorm: out [rows][dim] = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w)),
+ * fp32 throughout (elementwise.cuh:8-13). dim % 8 == 0. */
+int qw4_rmsnorm(uint16_t* out, const uint16_t* x, const uint16_t* w, int rows, int dim,
+                float eps, void* stream);
+/* residual_add: out[i] = bf16(out[i] + x[i]), i < n (elementwise.cuh:15-17). */
+int qw4_residual_add(uint16_t* out, const uint16_t* x, size_t n, void* stream);
+/* swiglu: out [rows][inter] = bf16(silu(g) * u) of a fused [rows][gate | up]
+ * buffer, silu(g) = g / (1 + exp(-g)) (elementwise.cuh:19-22). inter % 8 == 0. */
+int qw4_swiglu(uint16_t* out, const uint16_t* fused, int rows, int inter, void* stream);
+
+/* The same steps fused into the decode / verify GEMV (1 <= M <= 16), with the
+ * reference's roundings (each projection output rounded to bf16 first):
+ *
+ * linear then residual_add (model.cu:779-784): h [M][out_f] = bf16(h + bf16(x @ W^T)). */
+int qw4_gemv_residual(uint16_t* h, const qw4_weights* w, const uint16_t* x, int M,
+                      qw4_scratch* s, void* stream);
+/* linear over the fused [gate | up] weight (out_f = 2 * inter, inter % 64 == 0),
+ * then swiglu (model.cu:776-778): y [M][inter]. For M <= 2 (or tmp NULL) the
+ * intermediate [M][2 inter] is never written; for M > 2 with tmp
+ * ([M][2 inter] bf16) the projection goes through tmp and a separate swiglu,
+ * which is faster there. Same results either way. */
+int qw4_gemv_swiglu(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M, uint16_t* tmp,
+                    qw4_scratch* s, void* stream);
+/* rmsnorm then linear (model.cu:697-700, :773-777): y [M][out_f] = rmsnorm(h) @ W^T
+ * with norm weight norm_w [in_f]. The normalized rows are formed in LDS and
+ * never written; when they do not fit (M * in_f * 2 beyond the staging
+ * limit), tmp ([M][in_f] bf16, may be NULL otherwise) receives them and the
+ * plain GEMV follows. Results equal qw4_rmsnorm + qw4_gemm_small bit for bit. */
+int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
+                     const uint16_t* norm_w, float eps, int M, uint16_t* tmp, qw4_scratch* s,
+                     void* stream);
+
+/* ------------------------------------------------------------ dispatch
+ * linear() with lin_path() (src/model/model.cu:522-565, :643-658): T rows of
+ * x through the GEMV (T = 1), the skinny kernel in chunks of up to 16 rows
+ * (2 <= T <= max_t), or the prefill GEMM (T > max_t). max_t is the crossover
+ * measured on MI355X for this weight's size (qw4_linear_max_t: 48 rows for
+ * a 93 MB projection, 176 for an 11 MB one); env QW4_LIN_MAX_T overrides it,
+ * as QWEN_MMA_MAX_T does in the reference. ws may be NULL. */
+int qw4_linear(uint16_t* y, const qw4_weights* w, const uint16_t* x, int T, qw4_scratch* s,
+               qw4_workspace* ws, void* stream);
+int qw4_linear_max_t(const qw4_weights* w);
+
 /* ------------------------------------------------------ 8-bit weights
  * W8A16Weights (src/kernels/gemv_w4a16.cuh:141-154), the reference's default
  * lm_head format: per (row, 128-group) a bf16 scale and int8 q in [-127, 127].

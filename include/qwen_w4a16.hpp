@@ -128,4 +128,31 @@ void argmax(int32_t* out, const __hip_bfloat16* x, int n, int32_t* scratch,
             hipStream_t stream = 0);
 void argmax_rows(int32_t* out, const __hip_bfloat16* x, int rows, int n, hipStream_t stream = 0);
 
+// The layer steps either side of the projections (src/kernels/elementwise.cuh:8-22).
+void rmsnorm(__hip_bfloat16* out, const __hip_bfloat16* x, const __hip_bfloat16* w, int rows,
+             int dim, float eps, hipStream_t stream = 0);
+void residual_add(__hip_bfloat16* out, const __hip_bfloat16* x, int n, hipStream_t stream = 0);
+void swiglu(__hip_bfloat16* out, const __hip_bfloat16* fused, int rows, int inter,
+            hipStream_t stream = 0);
+
+// The same steps fused into the decode / verify GEMV, 1 <= M <= 16 (no
+// reference counterparts: the reference runs them as separate kernels around
+// linear(), src/model/model.cu:697-700, :772-785).
+//   h = bf16(h + bf16(x @ W^T))                         (linear + residual_add)
+void gemv_w4a16_residual(__hip_bfloat16* h, const W4A16Weights& w, const __hip_bfloat16* x,
+                         int M, GemvScratch& s, hipStream_t stream = 0);
+//   y = swiglu(x @ [gate | up]^T), y [M][out_f / 2]; tmp [M][out_f] (or
+//   nullptr) carries the projection for M > 2     (linear + swiglu)
+void gemv_w4a16_swiglu(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int M,
+                       __hip_bfloat16* tmp, GemvScratch& s, hipStream_t stream = 0);
+//   y = rmsnorm(h) @ W^T; tmp [M][in_f] is used when the rows do not fit the
+//   kernel's staging (may be nullptr otherwise)       (rmsnorm + linear)
+void gemv_w4a16_rmsnorm(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* h,
+                        const __hip_bfloat16* norm_w, float eps, int M, __hip_bfloat16* tmp,
+                        GemvScratch& s, hipStream_t stream = 0);
+
+// linear() with lin_path() (src/model/model.cu:522-565, :643-658) over T rows.
+void linear_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int T,
+                  GemvScratch& s, GemmWorkspace& ws, hipStream_t stream = 0);
+
 }  // namespace qwen

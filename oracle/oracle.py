@@ -301,6 +301,35 @@ def argmax_rows_bf16(v):
     return idx
 
 
+# ------------------------------------------------- layer steps either side
+# numpy restatements of the reference's elementwise kernels; bf16 in/out as
+# uint16 bits, fp32 arithmetic as the reference does it.
+def rmsnorm_bf16(x, w, eps):
+    """src/kernels/elementwise.cu:8-31: per row, inv = rsqrt(sum(x^2) / dim + eps)
+    (fp32 sum; here accumulated in float64, then rounded to fp32), then
+    bf16(x * inv * (1 + w)) in fp32."""
+    xf = bf16_to_f32(np.atleast_2d(x))
+    wf = bf16_to_f32(np.asarray(w)).astype(np.float32)
+    ss = np.sum(xf.astype(np.float64) ** 2, axis=1).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt(ss / np.float32(xf.shape[1]) + np.float32(eps))).astype(np.float32)
+    out = (xf * inv[:, None]).astype(np.float32) * (np.float32(1.0) + wf)[None, :]
+    return f32_to_bf16(out.astype(np.float32))
+
+
+def swiglu_bf16(fused, inter):
+    """src/kernels/elementwise.cu:40-49: bf16(g / (1 + exp(-g)) * u), fp32."""
+    f = bf16_to_f32(np.atleast_2d(fused)).astype(np.float32)
+    g, u = f[:, :inter], f[:, inter:2 * inter]
+    with np.errstate(over="ignore"):
+        out = (g / (np.float32(1.0) + np.exp(-g))) * u
+    return f32_to_bf16(out.astype(np.float32))
+
+
+def residual_add_bf16(out, x):
+    """src/kernels/elementwise.cu:34-37: bf16(out + x) in fp32."""
+    return f32_to_bf16((bf16_to_f32(out) + bf16_to_f32(x)).astype(np.float32))
+
+
 # ------------------------------------------------------------- tolerances
 def parity_metrics(y_bf16: np.ndarray, ref: np.ndarray) -> dict:
     """max-rel = max|y - ref| / max|ref| against the unrounded reference

@@ -234,4 +234,46 @@ void argmax_rows(int32_t* out, const __hip_bfloat16* x, int rows, int n, hipStre
   check(qw4_argmax_rows(out, u16(x), rows, n, stream), "argmax_rows");
 }
 
+void rmsnorm(__hip_bfloat16* out, const __hip_bfloat16* x, const __hip_bfloat16* w, int rows,
+             int dim, float eps, hipStream_t stream) {
+  check(qw4_rmsnorm(u16(out), u16(x), u16(w), rows, dim, eps, stream), "rmsnorm");
+}
+
+void residual_add(__hip_bfloat16* out, const __hip_bfloat16* x, int n, hipStream_t stream) {
+  check(n < 0 ? QW4_ERR_SHAPE : qw4_residual_add(u16(out), u16(x), (size_t)n, stream),
+        "residual_add");
+}
+
+void swiglu(__hip_bfloat16* out, const __hip_bfloat16* fused, int rows, int inter,
+            hipStream_t stream) {
+  check(qw4_swiglu(u16(out), u16(fused), rows, inter, stream), "swiglu");
+}
+
+void gemv_w4a16_residual(__hip_bfloat16* h, const W4A16Weights& w, const __hip_bfloat16* x,
+                         int M, GemvScratch& s, hipStream_t stream) {
+  const qw4_weights v = view(w);
+  check(qw4_gemv_residual(u16(h), &v, u16(x), M, &s.impl, stream), "gemv_w4a16_residual");
+}
+
+void gemv_w4a16_swiglu(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int M,
+                       __hip_bfloat16* tmp, GemvScratch& s, hipStream_t stream) {
+  const qw4_weights v = view(w);
+  check(qw4_gemv_swiglu(u16(y), &v, u16(x), M, u16(tmp), &s.impl, stream), "gemv_w4a16_swiglu");
+}
+
+void gemv_w4a16_rmsnorm(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* h,
+                        const __hip_bfloat16* norm_w, float eps, int M, __hip_bfloat16* tmp,
+                        GemvScratch& s, hipStream_t stream) {
+  const qw4_weights v = view(w);
+  check(qw4_gemv_rmsnorm(u16(y), &v, u16(h), u16(norm_w), eps, M, u16(tmp), &s.impl, stream),
+        "gemv_w4a16_rmsnorm");
+}
+
+void linear_w4a16(__hip_bfloat16* y, const W4A16Weights& w, const __hip_bfloat16* x, int T,
+                  GemvScratch& s, GemmWorkspace& ws, hipStream_t stream) {
+  const qw4_weights v = view(w);
+  qw4_workspace q{ws.wbuf, ws.bytes};
+  check(qw4_linear(u16(y), &v, u16(x), T, &s.impl, &q, stream), "linear_w4a16");
+}
+
 }  // namespace qwen

@@ -64,7 +64,17 @@ int check_weights_public(const qw4_weights* w);
 
 namespace {
 
-enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_ARGMAX = 2 };
+// Epilogues of the skinny kernels (k_rows takes every mode, k_skinny the
+// first three):
+//   OUT_BF16   y = bf16(acc)
+//   OUT_F32    y = acc
+//   OUT_ARGMAX the row argmax of acc (no logits written)
+//   OUT_RES    y = bf16(res + bf16(acc)): linear then residual_add
+//              (src/model/model.cu:781-783; y may be res)
+//   OUT_SWIGLU y = bf16(silu(bf16(acc_gate)) * bf16(acc_up)) over a fused
+//              [gate | up] weight: linear then swiglu (model.cu:776-778)
+//   OUT_NORM   bf16 y of rmsnorm(x): rmsnorm then linear (model.cu:773-777)
+enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_ARGMAX = 2, OUT_RES = 3, OUT_SWIGLU = 4, OUT_NORM = 5 };
 
 // Memory-side atomics on one cache line serialize; each counter gets its own line.
 constexpr int kCounterStride = 32;
@@ -94,6 +104,10 @@ struct SkinnyArgs {
   int M, N, K, G, tiles, max_tiles, P, U;
   uint32_t slot_bytes;
   uint32_t weight_bytes;   // packed weights (4- or 8-bit blocks)
+  const uint16_t* res;     // OUT_RES: residual [M][N] (may be y)
+  const uint16_t* nw;      // OUT_NORM: rmsnorm weight [K] (applied as 1 + w)
+  float eps;               // OUT_NORM: rmsnorm epsilon
+  int ld;                  // row stride of y (N; the intermediate size for OUT_SWIGLU)
 };
 
 // Monotonic key: larger value first, then lower index (elementwise.cu:103-104).
@@ -706,8 +720,15 @@ __device__ __forceinline__ void emit_rows(const SkinnyArgs& a, int b, int st0,
       continue;
     }
     if (m >= a.M) continue;
-    if (OUT == OUT_BF16) {
-      uint16_t* y = static_cast<uint16_t*>(a.y) + (size_t)m * a.N + n0;
+    if (OUT == OUT_RES) {
+      // bf16(res + bf16(acc)), the reference's linear then residual_add
+      uint16_t* y = static_cast<uint16_t*>(a.y) + (size_t)m * a.ld + n0;
+      const uint16_t* r = a.res + (size_t)m * a.ld + n0;
+#pragma unroll
+      for (int i = 0; i < S; ++i)
+        y[i] = to_bf16(bf16_bits_to_f32(r[i]) + bf16_bits_to_f32(to_bf16(acc[i][jj])));
+    } else if (OUT == OUT_BF16 || OUT == OUT_NORM) {
+      uint16_t* y = static_cast<uint16_t*>(a.y) + (size_t)m * a.ld + n0;
       if (S == 4)
         *reinterpret_cast<u32x2*>(y) = u32x2{pack_bf16x2(acc[0][jj], acc[1 % S][jj]),
                                              pack_bf16x2(acc[2 % S][jj], acc[3 % S][jj])};
@@ -716,10 +737,28 @@ __device__ __forceinline__ void emit_rows(const SkinnyArgs& a, int b, int st0,
       else
         *y = to_bf16(acc[0][jj]);
     } else {
-      float* y = static_cast<float*>(a.y) + (size_t)m * a.N + n0;
+      float* y = static_cast<float*>(a.y) + (size_t)m * a.ld + n0;
 #pragma unroll
       for (int i = 0; i < S; ++i) y[i] = acc[i][jj];
     }
+  }
+}
+
+
+// OUT_SWIGLU (wave 0): gate rows of tile b (the intermediate index), their up
+// rows' sums in u.
+template <int S>
+__device__ __forceinline__ void emit_swiglu(const SkinnyArgs& a, int b, int st0,
+                                            const f32x4 (&g)[S], const f32x4 (&u)[S], int lane) {
+  const int c = lane & 15, q = lane >> 4;
+  const int n0 = b * kTileN + 4 * c + st0;
+#pragma unroll
+  for (int jj = 0; jj < 4; ++jj) {
+    const int m = 4 * q + jj;
+    if (m >= a.M) continue;
+    uint16_t* y = static_cast<uint16_t*>(a.y) + (size_t)m * a.ld + n0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) y[i] = swiglu_bf16_bits(to_bf16(g[i][jj]), to_bf16(u[i][jj]));
   }
 }
 
@@ -750,7 +789,14 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   const int zsh = 16 * (c & 1);
   const uint32_t wbase = Fmt<FMT>::woff(q, c);
   const int p = blockIdx.x;
-  const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
+  // OUT_SWIGLU: units come in pairs (gate unit v, its up unit v + U / 2),
+  // numbered 2v and 2v + 1 and never split between workgroups
+  const int u0 = OUT == OUT_SWIGLU ? 2 * (int)((long long)p * (a.U / 2) / a.P) : range_start(a, p);
+  const int u1 =
+      OUT == OUT_SWIGLU ? 2 * (int)((long long)(p + 1) * (a.U / 2) / a.P) : range_start(a, p + 1);
+  auto real_unit = [&](int v) {
+    return OUT == OUT_SWIGLU ? ((v & 1) ? (v >> 1) + a.U / 2 : (v >> 1)) : v;
+  };
   const NibConst k = nib_const();
   Best bs;
   best_init(bs);
@@ -761,7 +807,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   int lu = u0, lg = wave;   // load cursor (wave-uniform)
   auto load_next = [&](RowsData<FMT, S, XL>& d) {
     const bool in = lu < u1;
-    const int b = in ? lu / kPer : 0, st0 = in ? (lu % kPer) * S : 0;
+    const int ru = real_unit(lu);
+    const int b = in ? ru / kPer : 0, st0 = in ? (ru % kPer) * S : 0;
     const int g = in ? lg : 0;
     rows_load<FMT, S, XL>(d, rs, in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk, g,
                           wbase + (uint32_t)st0 * kQuad, (uint32_t)(4 * c + st0) * 2u, zoff,
@@ -786,18 +833,57 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     // the LDS stores are conditional and the scheduler cannot sink the loads
     // behind the weights.
     const int n16 = a.M * a.K / 8;
-    u32x4 xv[kRowsXChunks];
+    u32x4 xv[kRowsXChunks], nv[OUT == OUT_NORM ? kRowsXChunks : 1];
     int xi[kRowsXChunks];
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.nw), 0, OUT == OUT_NORM ? a.K * 2 : 0, 0x00020000);
 #pragma unroll
     for (int j = 0; j < kRowsXChunks; ++j) {
       xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
       xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
+      if (OUT == OUT_NORM)
+        nv[j & (OUT == OUT_NORM ? 0xff : 0)] = __builtin_amdgcn_raw_buffer_load_b128(
+            rn, (uint32_t)(xi[j] % (a.K / 8)) * 16u, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     prime();
 #pragma unroll
     for (int j = 0; j < kRowsXChunks; ++j) xlds[xi[j]] = xv[j];
     __syncthreads();
+    if (OUT == OUT_NORM) {
+      // rmsnorm of each row in place (src/kernels/elementwise.cu:8-31):
+      // x * rsqrt(mean(x^2) + eps) * (1 + w), fp32, rounded to bf16 once.
+      // Wave m % W sums row m's squares in a fixed order.
+      __shared__ float rinv[16];
+      const int kc = a.K / 8;
+      for (int m = wave; m < a.M; m += W) {
+        float ss = 0.f;
+        for (int i = lane; i < kc; i += 64) {
+          const u32x4 v = xlds[m * kc + i];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float lo = bf16_bits_to_f32(v[e] & 0xffffu), hi = bf16_bits_to_f32(v[e] >> 16);
+            ss += lo * lo + hi * hi;
+          }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+        if (lane == 0) rinv[m] = rsqrtf(ss / (float)a.K + a.eps);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kRowsXChunks; ++j) {
+        const float inv = rinv[xi[j] / kc];
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t xw = xv[j][e], ww = nv[j & (OUT == OUT_NORM ? 0xff : 0)][e];
+          o[e] = pack_bf16x2(rmsnorm_f32(xw, ww, inv), rmsnorm_f32(xw >> 16, ww >> 16, inv));
+        }
+        xlds[xi[j]] = o;
+      }
+      __syncthreads();
+    }
   } else {
     prime();
   }
@@ -806,6 +892,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
 #pragma unroll
   for (int i = 0; i < S; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   int par = 0, closed = u0;
+  f32x4 gate[OUT == OUT_SWIGLU ? S : 1];   // OUT_SWIGLU: the gate unit's sums (wave 0)
   auto close_unit = [&]() {
 #pragma unroll
     for (int i = 0; i < S; ++i) red[par][wave][i][lane] = acc[i];
@@ -817,7 +904,20 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
       for (int w = 1; w < W; ++w)
 #pragma unroll
         for (int i = 0; i < S; ++i) t[i] += red[par][w][i][lane];
-      emit_rows<OUT, S>(a, closed / kPer, (closed % kPer) * S, t, lane, bs);
+      if (OUT == OUT_SWIGLU) {
+        const int gu = closed >> 1;   // the gate unit (= the output unit)
+        if ((closed & 1) == 0) {
+#pragma unroll
+          for (int i = 0; i < S; ++i) gate[i & (OUT == OUT_SWIGLU ? 0xff : 0)] = t[i];
+        } else {
+          f32x4 g[S];
+#pragma unroll
+          for (int i = 0; i < S; ++i) g[i] = gate[i & (OUT == OUT_SWIGLU ? 0xff : 0)];
+          emit_swiglu<S>(a, gu / kPer, (gu % kPer) * S, g, t, lane);
+        }
+      } else {
+        emit_rows<OUT, S>(a, closed / kPer, (closed % kPer) * S, t, lane, bs);
+      }
     }
     par ^= 1;
     ++closed;
@@ -827,7 +927,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
 
   int cg = wave;   // compute cursor: unit `closed`, group cg
   auto step = [&](RowsData<FMT, S, XL>& d, bool reload) {
-    rows_mma<FMT, S, XL>(acc, d, k, (closed % kPer) * S, zsh, xrow + cg * 16);
+    rows_mma<FMT, S, XL>(acc, d, k, (real_unit(closed) % kPer) * S, zsh, xrow + cg * 16);
     if (reload) load_next(d);
     cg += W;
     if (cg >= a.G) {
@@ -927,7 +1027,7 @@ constexpr int rows_depth() {
     if (W == 16) return 1;
     return XL ? (S == 1 ? 5 : (S == 2 ? 3 : 2)) : (S == 4 ? 1 : 2);
   }
-  if (W == 16) return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 1)) : 1;
+  if (W == 16) return XL ? (S == 1 ? 4 : (S == 2 ? (OUT == OUT_SWIGLU ? 2 : 3) : 1)) : 1;
   return XL ? (S == 1 ? 4 : (S == 2 ? 3 : 2)) : (S == 4 ? 2 : 3);
 }
 
@@ -994,7 +1094,8 @@ Launch launch_for(int out_f, int G, int M) {
   if (g_env_w == 4 || g_env_w == 8 || g_env_w == 16) l.W = g_env_w;
   long long cap;
   if (l.W == 4)
-    cap = (long long)device_cus() * wgs_per_cu<OUT, 4, M1, FMT>();
+    cap = (long long)device_cus() *
+          wgs_per_cu<OUT <= OUT_ARGMAX ? OUT : OUT_BF16, 4, M1, FMT>();   // k_skinny modes
   else
     cap = (long long)tiles * (l.W == 16 ? 2 : 1);
   if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
@@ -1017,9 +1118,12 @@ Launch launch_for(int out_f, int G, int M) {
   const char* ew = std::getenv("QW4_ROWS_W");
   const int env_rows_w = ew ? std::atoi(ew) : 0;
   l.XL = false;
-  if (env_rows == 0) return l;
+  if (env_rows == 0 && OUT <= OUT_ARGMAX) return l;   // stream-K has the basic epilogues only
+  // OUT_SWIGLU pairs a gate unit with its up unit in one workgroup: 32-row
+  // units keep as many workgroups as the plain GEMV's 64-row units
   l.S = (env_rows == 1 || env_rows == 2 || env_rows == 4) ? env_rows
-                                                          : (tiles < device_cus() ? 2 : 4);
+        : (OUT == OUT_SWIGLU || tiles < device_cus()) ? 2
+                                                      : 4;
   if (OUT == OUT_ARGMAX)
     l.W = 8;   // the running argmax does not fit 16 waves' registers
   else if (env_rows_w == 8 || env_rows_w == 16)
@@ -1045,7 +1149,8 @@ Launch launch_for(int out_f, int G, int M) {
   if (l.XL) occ = std::max(1, std::min(occ, kLdsBytes / (static_lds + xbytes)));
   long long pc = (long long)device_cus() * occ;
   if (env_p > 0) pc = env_p;
-  l.P = (int)std::max<long long>(1, std::min(units, pc));
+  // OUT_SWIGLU: whole (gate, up) unit pairs per workgroup
+  l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? units / 2 : units, pc));
   return l;
 }
 
@@ -1093,9 +1198,16 @@ struct WeightView {
   size_t weight_bytes;
 };
 
+// Epilogue inputs (see the OUT_* modes).
+struct Epi {
+  const uint16_t* res = nullptr;
+  const uint16_t* nw = nullptr;
+  float eps = 0.f;
+};
+
 template <int OUT, int FMT>
 int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scratch* s,
-               void* stream) {
+               void* stream, const Epi& e = Epi()) {
   if (!y || !x || !s || !s->counters || !s->partial || !s->keys) return QW4_ERR_NULL;
   if (M < 1 || M > 16) return QW4_ERR_M;
   if (((uintptr_t)x & 15) || ((uintptr_t)y & (OUT == OUT_F32 ? 15 : (OUT == OUT_BF16 ? 7 : 3))))
@@ -1130,28 +1242,40 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.U = tiles * w.G;
   a.slot_bytes = (uint32_t)(slot_floats() * 4);
   a.weight_bytes = (uint32_t)w.weight_bytes;
+  a.res = e.res;
+  a.nw = e.nw;
+  a.eps = e.eps;
+  a.ld = OUT == OUT_SWIGLU ? w.out_f / 2 : w.out_f;
+  if (OUT == OUT_SWIGLU && (w.out_f % (2 * kTileN))) return QW4_ERR_SHAPE;
+  if (OUT == OUT_NORM && !l.XL) return QW4_ERR_SHAPE;   // x must fit the LDS staging
+  if (OUT == OUT_RES && !e.res) return QW4_ERR_NULL;
+  if (OUT == OUT_NORM && (!e.nw || M > 16)) return QW4_ERR_NULL;
   if (l.S) {
     a.U = tiles * 4 / l.S;
     launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
     QW4_LAUNCH_CHECK();
     return QW4_OK;
   }
-  if (m1)
-    launch<OUT, true, FMT>(a, l.W, (hipStream_t)stream);
-  else
-    launch<OUT, false, FMT>(a, l.W, (hipStream_t)stream);
-  QW4_LAUNCH_CHECK();
-  return QW4_OK;
+  if constexpr (OUT <= OUT_ARGMAX) {
+    if (m1)
+      launch<OUT, true, FMT>(a, l.W, (hipStream_t)stream);
+    else
+      launch<OUT, false, FMT>(a, l.W, (hipStream_t)stream);
+    QW4_LAUNCH_CHECK();
+    return QW4_OK;
+  } else {
+    return QW4_ERR_SHAPE;   // unreachable: launch_for picks k_rows for these epilogues
+  }
 }
 
 template <int OUT>
 int run_skinny(void* y, const qw4_weights* w, const uint16_t* x, int M, qw4_scratch* s,
-               void* stream) {
+               void* stream, const Epi& e = Epi()) {
   const int st = check_weights_public(w);
   if (st) return st;
   const WeightView v{w->qweight, w->scale, w->zeros, w->out_f, w->in_f, w->num_groups,
                      (size_t)w->out_f * w->in_f / 2};
-  return run_skinny<OUT, 4>(y, v, x, M, s, stream);
+  return run_skinny<OUT, 4>(y, v, x, M, s, stream, e);
 }
 
 int check_w8(const qw4_w8_weights* w) {
@@ -1262,6 +1386,43 @@ int qw4_gemm_mma(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
 int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
                     qw4_scratch* s, void* stream) {
   return run_skinny<OUT_ARGMAX>(idx, w, x, M, s, stream);
+}
+
+int qw4_gemv_residual(uint16_t* h, const qw4_weights* w, const uint16_t* x, int M,
+                      qw4_scratch* s, void* stream) {
+  if (!h) return QW4_ERR_NULL;
+  Epi e;
+  e.res = h;
+  return run_skinny<OUT_RES>(h, w, x, M, s, stream, e);
+}
+
+int qw4_gemv_swiglu(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M, uint16_t* tmp,
+                    qw4_scratch* s, void* stream) {
+  // Fused for M <= 2; beyond, the pairing of gate and up rows in one
+  // workgroup is slower than the projection plus a separate swiglu (measured
+  // on MI355X), which runs through tmp when one is given.
+  if (M <= 2 || !tmp) return run_skinny<OUT_SWIGLU>(y, w, x, M, s, stream);
+  if (!w) return QW4_ERR_NULL;
+  if (w->out_f % (2 * kTileN)) return QW4_ERR_SHAPE;
+  const int st = run_skinny<OUT_BF16>(tmp, w, x, M, s, stream);
+  if (st) return st;
+  return qw4_swiglu(y, tmp, M, w->out_f / 2, stream);
+}
+
+int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
+                     const uint16_t* norm_w, float eps, int M, uint16_t* tmp, qw4_scratch* s,
+                     void* stream) {
+  if (!norm_w) return QW4_ERR_NULL;
+  Epi e;
+  e.nw = norm_w;
+  e.eps = eps;
+  const int st = run_skinny<OUT_NORM>(y, w, h, M, s, stream, e);
+  if (st != QW4_ERR_SHAPE || !tmp) return st;
+  // activations too large to stage: rmsnorm into tmp, then the plain GEMV
+  if (!w || !h) return QW4_ERR_NULL;
+  const int st2 = qw4_rmsnorm(tmp, h, norm_w, M, w->in_f, eps, stream);
+  if (st2) return st2;
+  return run_skinny<OUT_BF16>(y, w, tmp, M, s, stream);
 }
 
 int qw4_w8_gemv(uint16_t* y, const qw4_w8_weights* w, const uint16_t* x, qw4_scratch* s,

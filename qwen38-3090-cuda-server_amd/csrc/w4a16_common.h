@@ -90,6 +90,19 @@ __device__ __forceinline__ uint16_t to_bf16(float f) {
   return (uint16_t)(pack_bf16x2(f, 0.f) & 0xffffu);
 }
 
+// bf16(silu(g) * u) for bf16 g, u: silu(g) = g / (1 + exp(-g)) in fp32, the
+// reference's k_swiglu (src/kernels/elementwise.cu:40-49).
+__device__ __forceinline__ uint16_t swiglu_bf16_bits(uint32_t g, uint32_t u) {
+  const float gf = bf16_bits_to_f32(g & 0xffffu), uf = bf16_bits_to_f32(u & 0xffffu);
+  return to_bf16((gf / (1.f + expf(-gf))) * uf);
+}
+
+// bf16(x * inv * (1 + w)) for bf16 x, w: the rmsnorm output rounding of the
+// reference's k_rmsnorm (src/kernels/elementwise.cu:29-30).
+__device__ __forceinline__ float rmsnorm_f32(uint32_t x, uint32_t w, float inv) {
+  return bf16_bits_to_f32(x & 0xffffu) * inv * (1.0f + bf16_bits_to_f32(w & 0xffffu));
+}
+
 }  // namespace qw4
 
 // Host-side helpers shared by the C-ABI translation units.

@@ -44,6 +44,8 @@ EXPORTS = (
     "qw4_st_find", "qw4_st_last_error", "qw4_load_ct_fused",
     "qw4_w8_quantize", "qw4_w8_free", "qw4_w8_bytes", "qw4_w8_dequant_rows", "qw4_w8_gemv",
     "qw4_w8_gemm_small", "qw4_w8_gemv_argmax",
+    "qw4_rmsnorm", "qw4_residual_add", "qw4_swiglu", "qw4_gemv_residual", "qw4_gemv_swiglu",
+    "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -159,6 +161,14 @@ def lib():
         "qw4_w8_gemv": ([vp, W8, vp, S, vp], i),
         "qw4_w8_gemm_small": ([vp, W8, vp, i, S, vp], i),
         "qw4_w8_gemv_argmax": ([vp, W8, vp, i, S, vp], i),
+        "qw4_rmsnorm": ([vp, vp, vp, i, i, C.c_float, vp], i),
+        "qw4_residual_add": ([vp, vp, sz, vp], i),
+        "qw4_swiglu": ([vp, vp, i, i, vp], i),
+        "qw4_gemv_residual": ([vp, W, vp, i, S, vp], i),
+        "qw4_gemv_swiglu": ([vp, W, vp, i, vp, S, vp], i),
+        "qw4_gemv_rmsnorm": ([vp, W, vp, vp, C.c_float, i, vp, S, vp], i),
+        "qw4_linear": ([vp, W, vp, i, S, WS, vp], i),
+        "qw4_linear_max_t": ([W], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -322,6 +332,75 @@ def gemv_argmax_w4a16(idx, w: W4A16Weights, x, M: int, s: GemvScratch, stream=No
     _need(x, max(M, 0) * w.in_f * 2, "gemv_argmax_w4a16 x")
     _chk(lib().qw4_gemv_argmax(_ptr(idx), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
          "gemv_argmax_w4a16")
+
+
+# ------------------------------------------- layer steps either side
+def rmsnorm(out, x, w, rows: int, dim: int, eps: float, stream=None) -> None:
+    """rmsnorm (elementwise.cuh:8-13): out = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w))."""
+    _need(out, rows * dim * 2, "rmsnorm out")
+    _need(x, rows * dim * 2, "rmsnorm x")
+    _need(w, dim * 2, "rmsnorm w")
+    _chk(lib().qw4_rmsnorm(_ptr(out), _ptr(x), _ptr(w), rows, dim, eps, _stream(stream)),
+         "rmsnorm")
+
+
+def residual_add(out, x, n: int, stream=None) -> None:
+    """residual_add (elementwise.cuh:15-17): out[i] = bf16(out[i] + x[i])."""
+    _need(out, n * 2, "residual_add out")
+    _need(x, n * 2, "residual_add x")
+    _chk(lib().qw4_residual_add(_ptr(out), _ptr(x), n, _stream(stream)), "residual_add")
+
+
+def swiglu(out, fused, rows: int, inter: int, stream=None) -> None:
+    """swiglu (elementwise.cuh:19-22): out[r] = bf16(silu(gate[r]) * up[r])."""
+    _need(out, rows * inter * 2, "swiglu out")
+    _need(fused, rows * 2 * inter * 2, "swiglu fused")
+    _chk(lib().qw4_swiglu(_ptr(out), _ptr(fused), rows, inter, _stream(stream)), "swiglu")
+
+
+def gemv_residual_w4a16(h, w: W4A16Weights, x, M: int, s: GemvScratch, stream=None) -> None:
+    """linear then residual_add (model.cu:779-784): h = bf16(h + bf16(x @ W^T))."""
+    _need(h, max(M, 0) * w.out_f * 2, "gemv_residual h")
+    _need(x, max(M, 0) * w.in_f * 2, "gemv_residual x")
+    _chk(lib().qw4_gemv_residual(_ptr(h), C.byref(w), _ptr(x), M, C.byref(s), _stream(stream)),
+         "gemv_residual")
+
+
+def gemv_swiglu_w4a16(y, w: W4A16Weights, x, M: int, s: GemvScratch, tmp=None,
+                      stream=None) -> None:
+    """linear over a fused [gate | up] weight then swiglu (model.cu:776-778)."""
+    _need(y, max(M, 0) * (w.out_f // 2) * 2, "gemv_swiglu y")
+    _need(x, max(M, 0) * w.in_f * 2, "gemv_swiglu x")
+    if tmp is not None:
+        _need(tmp, max(M, 0) * w.out_f * 2, "gemv_swiglu tmp")
+    _chk(lib().qw4_gemv_swiglu(_ptr(y), C.byref(w), _ptr(x), M, _ptr(tmp), C.byref(s),
+                               _stream(stream)), "gemv_swiglu")
+
+
+def gemv_rmsnorm_w4a16(y, w: W4A16Weights, h, norm_w, eps: float, M: int, s: GemvScratch,
+                       tmp=None, stream=None) -> None:
+    """rmsnorm then linear (model.cu:697-700, :773-777)."""
+    _need(y, max(M, 0) * w.out_f * 2, "gemv_rmsnorm y")
+    _need(h, max(M, 0) * w.in_f * 2, "gemv_rmsnorm h")
+    _need(norm_w, w.in_f * 2, "gemv_rmsnorm norm_w")
+    if tmp is not None:
+        _need(tmp, max(M, 0) * w.in_f * 2, "gemv_rmsnorm tmp")
+    _chk(lib().qw4_gemv_rmsnorm(_ptr(y), C.byref(w), _ptr(h), _ptr(norm_w), eps, M, _ptr(tmp),
+                                C.byref(s), _stream(stream)), "gemv_rmsnorm")
+
+
+def linear_w4a16(y, w: W4A16Weights, x, T: int, s: GemvScratch, ws: GemmWorkspace | None = None,
+                 stream=None) -> None:
+    """linear() with lin_path() (model.cu:522-565, :643-658)."""
+    _need(y, max(T, 0) * w.out_f * 2, "linear y")
+    _need(x, max(T, 0) * w.in_f * 2, "linear x")
+    _chk(lib().qw4_linear(_ptr(y), C.byref(w), _ptr(x), T, C.byref(s),
+                          C.byref(ws) if ws is not None else None, _stream(stream)), "linear")
+
+
+def linear_max_t(w: W4A16Weights) -> int:
+    """Rows up to which linear() uses 16-row skinny passes for this weight."""
+    return lib().qw4_linear_max_t(C.byref(w))
 
 
 # ------------------------------------------------------- 8-bit lm_head

@@ -142,6 +142,57 @@ int main() {
   std::printf("argmax_rows      %s\n", am ? "ok" : "FAIL");
   fails += !am;
 
+  // layer steps around the projections (src/model/model.cu:772-785): each
+  // fused entry point equals the unfused steps bit for bit, and linear()
+  // equals the path it dispatches to
+  {
+    auto bf = [](uint16_t* p) { return reinterpret_cast<__hip_bfloat16*>(p); };
+    const size_t yb = (size_t)M * N * 2;
+    std::vector<uint16_t> h0((size_t)M * N), nwh(K);
+    for (auto& v : h0) v = or_f32_to_bf16(nd(rng));
+    for (auto& v : nwh) v = or_f32_to_bf16(nd(rng) * 0.1f);
+    uint16_t *d_h = upload(h0), *d_h2 = upload(h0), *d_nw = upload(nwh);
+    uint16_t *d_a = nullptr, *d_b = nullptr, *d_t = nullptr;
+    CK(hipMalloc(&d_a, yb));
+    CK(hipMalloc(&d_b, yb));
+    CK(hipMalloc(&d_t, (size_t)M * K * 2));
+    std::vector<uint16_t> ua((size_t)M * N), ub((size_t)M * N);
+    auto same = [&](const char* what, uint16_t* p, uint16_t* q, size_t n) {
+      std::vector<uint16_t> a(n), b(n);
+      if (hipMemcpy(a.data(), p, n * 2, hipMemcpyDeviceToHost) != hipSuccess ||
+          hipMemcpy(b.data(), q, n * 2, hipMemcpyDeviceToHost) != hipSuccess)
+        return false;
+      const bool ok = std::memcmp(a.data(), b.data(), n * 2) == 0;
+      std::printf("%-16s %s\n", what, ok ? "bit-exact" : "FAIL");
+      return ok;
+    };
+    // linear + residual_add
+    qwen::gemv_w4a16_residual(bf(d_h), W, bf(d_x), M, S);
+    qwen::gemm_small_w4a16(bf(d_a), W, bf(d_x), M, S);
+    qwen::residual_add(bf(d_h2), bf(d_a), M * N);
+    fails += !same("gemv_residual", d_h, d_h2, (size_t)M * N);
+    // linear + swiglu over [gate | up] (out_f = 2 x 256)
+    qwen::gemv_w4a16_swiglu(bf(d_a), W, bf(d_x), M, nullptr, S);
+    qwen::gemm_small_w4a16(bf(d_b), W, bf(d_x), M, S);
+    qwen::swiglu(bf(d_t), bf(d_b), M, N / 2);
+    fails += !same("gemv_swiglu", d_a, d_t, (size_t)M * N / 2);
+    // rmsnorm + linear (M = 1: staged in LDS)
+    qwen::gemv_w4a16_rmsnorm(bf(d_a), W, bf(d_x), bf(d_nw), 1e-6f, 1, d_t ? bf(d_t) : nullptr, S);
+    qwen::rmsnorm(bf(d_t), bf(d_x), bf(d_nw), 1, K, 1e-6f);
+    qwen::gemv_w4a16(bf(d_b), W, bf(d_t), S);
+    fails += !same("gemv_rmsnorm", d_a, d_b, (size_t)N);
+    // linear(): T = M -> 16-row skinny pass, T = Mp -> (by size) skinny or GEMM
+    qwen::linear_w4a16(bf(d_a), W, bf(d_x), M, S, ws);
+    qwen::gemm_small_w4a16(bf(d_b), W, bf(d_x), M, S);
+    fails += !same("linear T=9", d_a, d_b, (size_t)M * N);
+    CK(hipFree(d_h));
+    CK(hipFree(d_h2));
+    CK(hipFree(d_nw));
+    CK(hipFree(d_a));
+    CK(hipFree(d_b));
+    CK(hipFree(d_t));
+  }
+
   qwen::gemm_workspace_free(ws);
   qwen::gemv_scratch_free(S);
   qwen::awq_free(W);

@@ -118,3 +118,16 @@ def test_cpp_layer_exports_every_declared_function(hip):
     out = subprocess.run(["nm", "-DC", hip.LIB_PATH], capture_output=True, text=True).stdout
     defined = set(re.findall(r" T qwen::([a-z_0-9]+)\(", out))
     assert len(names) >= 20 and names <= defined, names - defined
+
+
+def test_linear_threshold_by_weight_size(hip, monkeypatch):
+    """linear()'s skinny/prefill crossover per weight (host-only call): the
+    model's projections get 48 (gate|up), 80 (down), 144 (qkv), 176 (o_proj)."""
+    monkeypatch.delenv("QW4_LIN_MAX_T", raising=False)
+    want = {(34816, 5120): 48, (5120, 17408): 80, (7168, 5120): 144, (5120, 4096): 176}
+    for (n, k), t in want.items():
+        w = hip.W4A16Weights()
+        w.out_f, w.in_f, w.group_size, w.num_groups = n, k, 128, k // 128
+        assert hip.linear_max_t(w) == t, (n, k)
+    monkeypatch.setenv("QW4_LIN_MAX_T", "33")
+    assert hip.linear_max_t(w) == 33
