@@ -338,6 +338,48 @@ class Bench:
         self.extra["config5_lm_head_w8_argmax"] = c5w8
         hip.w8a16_free(w8)
         log(f"config5 w8: {c5w8}")
+        self.layer_steps()
+
+    # ------------------------------------------- fused steps around the GEMVs
+    def layer_steps(self):
+        """The layer's elementwise steps (src/model/model.cu:772-785) fused into
+        the decode GEMV vs run as separate kernels, M = 1, over 16 of the sweep's
+        layers (graph replays, per layer)."""
+        hip, torch, scratch = self.hip, self.torch, self.scratch
+        lw = self.layers[:16]
+        x5, x17 = self.xs[5120], self.xs[17408]
+        inter = torch.empty(34816, dtype=torch.int16, device="cuda")
+        act = torch.empty(17408, dtype=torch.int16, device="cuda")
+        h = torch.empty(5120, dtype=torch.int16, device="cuda")
+        hip.gen_bf16(h, 5120, 0, 77, 0)
+        h2 = torch.empty(5120, dtype=torch.int16, device="cuda")
+        nw = torch.zeros(5120, dtype=torch.int16, device="cuda")
+        xn = torch.empty(5120, dtype=torch.int16, device="cuda")
+        yq = torch.empty(7168, dtype=torch.int16, device="cuda")
+
+        def per_layer(fn):
+            g = self.capture(lambda: [fn(w) for w in lw])
+            self.time_graph(g, 2)
+            t = self.time_graph(g, 5) / len(lw) * 1e3
+            del g
+            return round(t, 2)
+
+        steps = {
+            "rmsnorm+qkv": (
+                lambda w: (hip.rmsnorm(xn, h, nw, 1, 5120, 1e-6), hip.gemv_w4a16(yq, w[0], xn, scratch)),
+                lambda w: hip.gemv_rmsnorm_w4a16(yq, w[0], h, nw, 1e-6, 1, scratch)),
+            "gate|up+swiglu": (
+                lambda w: (hip.gemv_w4a16(inter, w[2], x5, scratch), hip.swiglu(act, inter, 1, 17408)),
+                lambda w: hip.gemv_swiglu_w4a16(act, w[2], x5, 1, scratch)),
+            "down+residual": (
+                lambda w: (hip.gemv_w4a16(h2, w[3], x17, scratch), hip.residual_add(h, h2, 5120)),
+                lambda w: hip.gemv_residual_w4a16(h, w[3], x17, 1, scratch)),
+        }
+        out = {}
+        for name, (sep, fus) in steps.items():
+            out[name] = {"separate_us": per_layer(sep), "fused_us": per_layer(fus)}
+        self.extra["layer_steps_m1"] = out
+        log(f"layer steps: {out}")
 
     # ---------------------------------------------------------- config 4
     def prefill(self):
