@@ -52,6 +52,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <type_traits>
 
 #include "../../include/qwen_w4a16.h"
 #include "w4a16_common.h"
@@ -608,8 +609,10 @@ __global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
 // at the end but the stores. Small units (S = 1: 16 rows) balance a launch
 // over the CUs where whole 64-row tiles cannot.
 // k_rows with activations in LDS: at most this many 16-byte chunks per thread
-// (M K 2 <= kRowsXChunks * 16 * 64 W bytes).
+// (M K 2 <= kRowsXChunks * 16 * 64 W bytes); twice as many with LDS-DMA items
+// (no item registers).
 constexpr int kRowsXChunks = 4;
+constexpr int rows_xchunks(bool dma) { return dma ? 2 * kRowsXChunks : kRowsXChunks; }
 constexpr int kLdsBytes = 160 * 1024;   // LDS per CU on gfx950
 
 
@@ -655,9 +658,99 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
   if (FMT == 4) d.z = __builtin_amdgcn_raw_buffer_load_b32(r.zr, zoff, blk * 32u, 0);
 }
 
-// XL: activations come from LDS (xl: this lane's row, k chunk q, group g);
-// otherwise from the registers rows_load filled.
+// ---- LDS-DMA items (k_rows with DMA): the weight, scale and zero-point
+// loads of an item go straight into an LDS slot of the wave (buffer_load ...
+// lds, lane i's bytes at slot + i * size), so the number of items in flight is
+// bounded by LDS, not by registers. The compiler does not order LDS reads
+// after these loads: each item waits with an explicit vmcnt (the loads issued
+// after it, which complete after it) before reading its slot.
+// Slot layout (16-byte units): NQ x 64 weight chunks, then 256 bytes of scales
+// (lane l: the scale word l & 31 of the 64-row block), then 256 bytes of zero
+// points (lane l: word l & 7; 4-bit formats only).
+template <int FMT, int S>
+struct DmaSlot {
+  static constexpr int kH = FMT == 8 ? 2 : 1;          // 16-byte chunks per row quad
+  static constexpr int kNQ = S * kH;                     // weight loads per item
+  static constexpr int kLoads = kNQ + 1 + (FMT == 4);    // loads per item
+  static constexpr int kUnits = kNQ * 64 + 16 + (FMT == 4 ? 16 : 0);
+};
+
+// 16 bytes per lane, nontemporal (weights); 4 bytes per lane (metadata)
+__device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff,
+                                           uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, kWeightAux);
+}
+__device__ __forceinline__ void dma_load4(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff,
+                                          uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4,
+                                           voff, soff, 0, 0);
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Workgroup barrier for LDS data written by ds_write. With LDS-DMA loads in
+// flight __syncthreads() would also wait for all of them (its fence counts
+// them as LDS writes); the unit sums only need this wave's LDS writes done.
+template <bool DMA>
+__device__ __forceinline__ void lds_barrier() {
+  if constexpr (DMA)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  else
+    __syncthreads();
+}
+
+template <int J, int D, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (J < D) {
+    f(std::integral_constant<int, J>{});
+    static_for<J + 1, D>(f);
+  }
+}
+
+template <int FMT, int S>
+__device__ __forceinline__ void dma_issue(u32x4* slot, const SkinnyRsrc& r, uint32_t blk,
+                                          uint32_t woff, int lane) {
+  using L = DmaSlot<FMT, S>;
+  constexpr uint32_t kBlk = FMT == 8 ? 8192u : 4096u;
+  constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
+#pragma unroll
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int h = 0; h < L::kH; ++h)
+      dma_load16(r.qw, slot + (i * L::kH + h) * 64, woff + i * kQuad + h * 16, blk * kBlk);
+  dma_load4(r.sc, slot + L::kNQ * 64, (uint32_t)(lane & 31) * 4u, blk * 128u);
+  if (FMT == 4) dma_load4(r.zr, slot + L::kNQ * 64 + 16, (uint32_t)(lane & 7) * 4u, blk * 32u);
+}
+
 template <int FMT, int S, bool XL>
+__device__ __forceinline__ void dma_read(RowsData<FMT, S, XL>& d, const u32x4* slot, int lane,
+                                         int st0) {
+  using L = DmaSlot<FMT, S>;
+  const int c = lane & 15;
+#pragma unroll
+  for (int i = 0; i < S; ++i)
+#pragma unroll
+    for (int h = 0; h < L::kH; ++h) d.w[i][h] = slot[(i * L::kH + h) * 64 + lane];
+  const uint32_t* sm = reinterpret_cast<const uint32_t*>(slot + L::kNQ * 64);
+  if (S == 4) {
+    d.s[0] = sm[2 * c];
+    d.s[(S + 1) / 2 - 1] = sm[2 * c + 1];
+  } else {
+    d.s[0] = sm[(4 * c + st0) >> 1];
+  }
+  if (FMT == 4) d.z = reinterpret_cast<const uint32_t*>(slot + L::kNQ * 64 + 16)[c >> 1];
+}
+
+// XL: activations come from LDS (xl: this lane's row, k chunk q, group g);
+// otherwise from the registers rows_load filled. JJ: the output rows
+// m = 4q + jj, jj < JJ, that are accumulated (M = 1: only jj = 0 is read).
+template <int FMT, int S, bool XL, int JJ = 4>
 __device__ __forceinline__ void rows_mma(f32x4 (&acc)[S], const RowsData<FMT, S, XL>& d, NibConst k,
                                          int st0, int zsh, const u32x4* xl) {
   const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
@@ -702,7 +795,7 @@ __device__ __forceinline__ void rows_mma(f32x4 (&acc)[S], const RowsData<FMT, S,
 #pragma unroll
   for (int i = 0; i < S; ++i)
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) acc[i][jj] += sf[i] * (C[i][jj] - zf[i] * Cs[jj]);
+    for (int jj = 0; jj < JJ; ++jj) acc[i][jj] += sf[i] * (C[i][jj] - zf[i] * Cs[jj]);
 }
 
 // Final values of one unit (wave 0): rows m = 4q + jj, columns b*64 + 4c + st0 + i.
@@ -774,11 +867,18 @@ __device__ __forceinline__ void emit_swiglu(const SkinnyArgs& a, int b, int st0,
 // and passes one barrier, so the waves stay in step for any G; wave 0 then
 // sums the W partials in wave order and emits the unit. No workgroup depends
 // on another.
-template <int OUT, int FMT, int S, int W, bool XL, int D>
+// DMA (with XL, M = 1): items are loaded into LDS slots (DmaSlot) instead of
+// registers, D per wave after the staged activations; the one output row sits
+// in lanes 0..15 (element jj = 0), so only those lanes take part in the unit
+// sums and only that element is accumulated.
+template <int OUT, int FMT, int S, int W, bool XL, int D, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
+  static_assert(!DMA || XL, "LDS-DMA items need the staged activations");
   constexpr int kPer = 4 / S;   // units per tile
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
-  __shared__ f32x4 red[2][W][S][64];
+  constexpr int kRedLanes = DMA ? 16 : 64;
+  constexpr int kXC = rows_xchunks(DMA);
+  __shared__ f32x4 red[2][W][S][kRedLanes];
   extern __shared__ u32x4 xlds[];
   // wave-uniform (scalar) so the item cursors live in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -820,11 +920,31 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     }
   };
 
-  RowsData<FMT, S, XL> buf[D];
+  RowsData<FMT, S, XL> buf[DMA ? 1 : D];
+  u32x4* const ring = xlds + a.M * a.K / 8 + wave * D * DmaSlot<FMT, S>::kUnits;
+  auto load_slot = [&](int j) {
+    const bool in = lu < u1;
+    const int ru = real_unit(lu);
+    const int b = in ? ru / kPer : 0, st0 = in ? (ru % kPer) * S : 0;
+    const int g = in ? lg : 0;
+    dma_issue<FMT, S>(ring + j * DmaSlot<FMT, S>::kUnits, rs,
+                      in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk,
+                      wbase + (uint32_t)st0 * kQuad, lane);
+    lg += W;
+    if (lg >= a.G) {
+      lg = wave;
+      ++lu;
+    }
+  };
   const u32x4* xrow = xlds + ((c < a.M ? c : a.M - 1) * a.K + 32 * q) / 8;
   auto prime = [&]() {
 #pragma unroll
-    for (int j = 0; j < D; ++j) load_next(buf[j]);
+    for (int j = 0; j < D; ++j) {
+      if constexpr (DMA)
+        load_slot(j);
+      else
+        load_next(buf[j & (DMA ? 0 : 0xff)]);
+    }
   };
   if (XL) {
     // x loads first, then the first weight items: waiting for x leaves the
@@ -833,12 +953,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     // the LDS stores are conditional and the scheduler cannot sink the loads
     // behind the weights.
     const int n16 = a.M * a.K / 8;
-    u32x4 xv[kRowsXChunks], nv[OUT == OUT_NORM ? kRowsXChunks : 1];
-    int xi[kRowsXChunks];
+    u32x4 xv[kXC], nv[OUT == OUT_NORM ? kXC : 1];
+    int xi[kXC];
     const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(a.nw), 0, OUT == OUT_NORM ? a.K * 2 : 0, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < kRowsXChunks; ++j) {
+    for (int j = 0; j < kXC; ++j) {
       xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
       xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
       if (OUT == OUT_NORM)
@@ -848,8 +968,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     prime();
 #pragma unroll
-    for (int j = 0; j < kRowsXChunks; ++j) xlds[xi[j]] = xv[j];
-    __syncthreads();
+    for (int j = 0; j < kXC; ++j) xlds[xi[j]] = xv[j];
+    lds_barrier<DMA>();
     if (OUT == OUT_NORM) {
       // rmsnorm of each row in place (src/kernels/elementwise.cu:8-31):
       // x * rsqrt(mean(x^2) + eps) * (1 + w), fp32, rounded to bf16 once.
@@ -870,9 +990,9 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
         for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
         if (lane == 0) rinv[m] = rsqrtf(ss / (float)a.K + a.eps);
       }
-      __syncthreads();
+      lds_barrier<DMA>();
 #pragma unroll
-      for (int j = 0; j < kRowsXChunks; ++j) {
+      for (int j = 0; j < kXC; ++j) {
         const float inv = rinv[xi[j] / kc];
         u32x4 o;
 #pragma unroll
@@ -882,7 +1002,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
         }
         xlds[xi[j]] = o;
       }
-      __syncthreads();
+      lds_barrier<DMA>();
     }
   } else {
     prime();
@@ -894,16 +1014,19 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   int par = 0, closed = u0;
   f32x4 gate[OUT == OUT_SWIGLU ? S : 1];   // OUT_SWIGLU: the gate unit's sums (wave 0)
   auto close_unit = [&]() {
+    if (!DMA || lane < kRedLanes) {
 #pragma unroll
-    for (int i = 0; i < S; ++i) red[par][wave][i][lane] = acc[i];
-    __syncthreads();
+      for (int i = 0; i < S; ++i) red[par][wave][i][lane % kRedLanes] = acc[i];
+    }
+    lds_barrier<DMA>();
     if (wave == 0) {
+      const int rl = lane % kRedLanes;
       f32x4 t[S];
 #pragma unroll
-      for (int i = 0; i < S; ++i) t[i] = red[par][0][i][lane];
+      for (int i = 0; i < S; ++i) t[i] = red[par][0][i][rl];
       for (int w = 1; w < W; ++w)
 #pragma unroll
-        for (int i = 0; i < S; ++i) t[i] += red[par][w][i][lane];
+        for (int i = 0; i < S; ++i) t[i] += red[par][w][i][rl];
       if (OUT == OUT_SWIGLU) {
         const int gu = closed >> 1;   // the gate unit (= the output unit)
         if ((closed & 1) == 0) {
@@ -939,15 +1062,50 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   // would make the compiler's wait counts assume the shortest path), then
   // the last < D items, already loaded
   int t0 = 0;
-  for (; t0 + D <= T; t0 += D) {
+  if constexpr (DMA) {
+    // item t waits for its slot; the loads of the items after it (all D - 1
+    // of them in the main loop, fewer in the tail) may still be in flight
+    constexpr int kL = DmaSlot<FMT, S>::kLoads;
+    auto step_dma = [&](auto jc, auto nc, bool reload) {
+      constexpr int j = decltype(jc)::value;
+      wait_vm<decltype(nc)::value>();
+      const int st0 = (real_unit(closed) % kPer) * S;
+      RowsData<FMT, S, XL> d;
+      dma_read<FMT, S, XL>(d, ring + j * DmaSlot<FMT, S>::kUnits, lane, st0);
+      rows_mma<FMT, S, XL, 1>(acc, d, k, st0, zsh, xrow + cg * 16);
+      if (reload) {
+        // the slot's LDS reads have returned before it is loaded again
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        load_slot(j);
+      }
+      cg += W;
+      if (cg >= a.G) {
+        cg = wave;
+        close_unit();
+      }
+    };
+    for (; t0 + D <= T; t0 += D)
+      static_for<0, D>([&](auto jc) {
+        step_dma(jc, std::integral_constant<int, (D - 1) * kL>{}, true);
+      });
+    static_for<0, D - 1>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      if (t0 + j < T) step_dma(jc, std::integral_constant<int, (D - 1 - j) * kL>{}, false);
+    });
+  } else {
+    for (; t0 + D <= T; t0 += D) {
 #pragma unroll
-    for (int j = 0; j < D; ++j) step(buf[j], true);
+      for (int j = 0; j < D; ++j) step(buf[j & (DMA ? 0 : 0xff)], true);
+    }
+#pragma unroll
+    for (int j = 0; j < D - 1; ++j)
+      if (t0 + j < T) step(buf[j & (DMA ? 0 : 0xff)], false);
   }
-#pragma unroll
-  for (int j = 0; j < D - 1; ++j)
-    if (t0 + j < T) step(buf[j], false);
   while (closed < u1) close_unit();   // waves with no items (wave >= G)
   if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
+  // loads issued past the last item land in LDS: done before the workgroup
+  // releases it
+  if constexpr (DMA) wait_vm<0>();
 }
 
 // ------------------------------------------------------------- host side
@@ -1010,6 +1168,7 @@ struct Launch {
   int W, P;
   int S;    // 0: stream-K (k_skinny); 1, 2, 4: k_rows with units of S row quads
   bool XL;  // k_rows: activations staged in LDS
+  int DMA = 0;   // k_rows: items in LDS slots, this many per wave (0: registers)
 };
 
 // Items each k_rows wave keeps in flight (the one being computed included),
@@ -1151,6 +1310,33 @@ Launch launch_for(int out_f, int G, int M) {
   if (env_p > 0) pc = env_p;
   // OUT_SWIGLU: whole (gate, up) unit pairs per workgroup
   l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? units / 2 : units, pc));
+  // M = 1: LDS-DMA items with 32-row units and 8 waves, when the slots fit
+  // the CU's LDS next to the staged activations. Measured on MI355X over the
+  // model's projections and heads: 4 items per wave when the output has at
+  // least as many 64-row tiles as CUs, 3 for long K (>= 64 groups), else 2
+  // (deeper is slower); the 4-bit GEMV and its residual / swiglu / argmax
+  // epilogues gain up to 8%, while the fused rmsnorm and the 8-bit head run
+  // faster with register items, which stay their default. QW4_DMA = 0 keeps
+  // register items, 2 | 3 | 4 forces LDS-DMA items of that depth for every
+  // mode (read on every call); QW4_ROWS / QW4_ROWS_W other than 2 / 8 keep
+  // register items.
+  if (M == 1 && (env_rows < 0 || env_rows == 2) && (env_rows_w == 0 || env_rows_w == 8)) {
+    const char* ed = std::getenv("QW4_DMA");
+    const int dd = ed ? std::atoi(ed)
+                   : (OUT == OUT_NORM || FMT == 8) ? 0
+                                                   : (tiles >= device_cus() ? 4 : (G >= 64 ? 3 : 2));
+    const int slot = (FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256);
+    const int need = xbytes + 8 * dd * slot + 2 * 8 * 2 * 16 * 16 + (OUT == OUT_NORM ? 64 : 0);
+    if (dd >= 2 && dd <= 4 && xbytes <= rows_xchunks(true) * 16 * 64 * 8 && need <= kLdsBytes) {
+      l.DMA = dd;
+      l.S = 2;
+      l.W = 8;
+      l.XL = true;
+      const long long u2 = (long long)tiles * 2;
+      const long long pc2 = (long long)device_cus() * (kLdsBytes / need);
+      l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, pc2));
+    }
+  }
   return l;
 }
 
@@ -1165,8 +1351,43 @@ void launch_rows_x(const SkinnyArgs& a, int S, hipStream_t st) {
     k_rows<OUT, FMT, 1, W, XL, rows_depth<OUT, FMT, 1, XL, W>()><<<a.P, 64 * W, lds, st>>>(a);
 }
 
+// Dynamic LDS above the default limit is allowed once per kernel.
+template <class K>
+void allow_lds(K kern, int bytes) {
+  static int set[64] = {0};
+  int& v = set[current_device()];
+  if (bytes > v) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess)
+      v = bytes;
+  }
+}
+
+template <int OUT, int FMT, int S, int W, int D>
+void launch_rows_dma_d(const SkinnyArgs& a, hipStream_t st) {
+  const int lds = a.M * a.K * 2 + W * D * DmaSlot<FMT, S>::kUnits * 16;
+  auto kern = k_rows<OUT, FMT, S, W, true, D, true>;
+  allow_lds(kern, lds);
+  kern<<<a.P, 64 * W, lds, st>>>(a);
+}
+
+// M = 1 with LDS-DMA items: 32-row units, 8 waves, D items per wave
+template <int OUT, int FMT>
+void launch_rows_dma(const SkinnyArgs& a, int D, hipStream_t st) {
+  if (D == 2)
+    launch_rows_dma_d<OUT, FMT, 2, 8, 2>(a, st);
+  else if (D == 3)
+    launch_rows_dma_d<OUT, FMT, 2, 8, 3>(a, st);
+  else
+    launch_rows_dma_d<OUT, FMT, 2, 8, 4>(a, st);
+}
+
 template <int OUT, int FMT>
 void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
+  if (l.DMA) {
+    launch_rows_dma<OUT, FMT>(a, l.DMA, st);
+    return;
+  }
   if (OUT == OUT_ARGMAX || l.W == 8)
     l.XL ? launch_rows_x<OUT, FMT, 8, true>(a, l.S, st) : launch_rows_x<OUT, FMT, 8, false>(a, l.S, st);
   else

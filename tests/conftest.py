@@ -21,13 +21,16 @@ def orc():
     return oracle
 
 
-@pytest.fixture(params=["rows", "streamk"])
+@pytest.fixture(params=["rows", "regs", "streamk"])
 def decode_path(request, monkeypatch):
-    """Runs a decode/verify test through both skinny kernels: the default
-    data-parallel k_rows and the stream-K kernel (QW4_ROWS=0, read by the
-    library on every call)."""
+    """Runs a decode/verify test through every skinny kernel form: the default
+    data-parallel k_rows (M = 1: items loaded straight into LDS), k_rows with
+    items in registers (QW4_DMA=0) and the stream-K kernel (QW4_ROWS=0); the
+    library reads both variables on every call."""
+    monkeypatch.delenv("QW4_ROWS", raising=False)
+    monkeypatch.delenv("QW4_DMA", raising=False)
     if request.param == "streamk":
         monkeypatch.setenv("QW4_ROWS", "0")
-    else:
-        monkeypatch.delenv("QW4_ROWS", raising=False)
+    elif request.param == "regs":
+        monkeypatch.setenv("QW4_DMA", "0")
     return request.param

@@ -1,0 +1,218 @@
+"""GPU parity of the decode kernel's LDS-DMA items (M = 1: the weight, scale and
+zero-point loads of each item go straight into LDS; QW4_DMA = items per wave,
+0 = items in registers) through the C-ABI entry points that take M = 1:
+gemv_w4a16 / _f32, the fused residual / swiglu / rmsnorm forms, the argmax
+heads and the W8A16 GEMV (src/kernels/gemv_w4a16.cuh:88-92, :112-118,
+:147-166; src/kernels/elementwise.cuh:34-43; src/model/model.cu:697-700,
+:772-785).
+
+Bar: bit-exact against the register-item kernel. For the same unit size and
+waves both do the same per-unit arithmetic in the same order (only which
+workgroup owns which unit differs), so any difference is a load or wait
+error. The oracle checks of the default path (DMA at M = 1) are in
+test_gpu_parity, test_gpu_fused and test_gpu_w8; one more here per shape
+class (the GEMV bars: max-rel 1e-2, mean-abs 1e-3)."""
+import numpy as np
+import pytest
+
+from gpu_util import dev, empty, host, repack_from_logical
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def hip():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU test run without a GPU"
+    import w4a16_hip
+
+    w4a16_hip.lib()
+    return w4a16_hip
+
+
+@pytest.fixture(scope="module")
+def scratch(hip):
+    s = hip.gemv_scratch_alloc(17408, 248320, 128, 16)
+    yield s
+    hip.gemv_scratch_free(s)
+
+
+def _sync():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def _gen(hip, N, K, seed):
+    """Device-generated AWQ tensor, repacked (large shapes without the oracle)."""
+    import torch
+
+    G = K // 128
+    q = torch.empty(K // 8 * N, dtype=torch.int32, device="cuda")
+    s = torch.empty(G * N, dtype=torch.int16, device="cuda")
+    z = torch.empty(G * N // 8, dtype=torch.int32, device="cuda")
+    hip.gen_awq_k(q, s, z, N, K, seed, 3)
+    w = hip.awq_alloc_fused(N, K)
+    hip.awq_repack_awq_into(w, 0, q, s, z, N, hip.LAYOUT_AWQ_K)
+    _sync()
+    return w
+
+
+def _x(hip, n, sid):
+    import torch
+
+    x = torch.empty(n, dtype=torch.int16, device="cuda")
+    hip.gen_bf16(x, n, 0, sid, 0)
+    return x
+
+
+def _both(monkeypatch, run):
+    """run() with register items (32-row units, 8 waves) and with LDS-DMA items
+    at every depth; every result must equal the first."""
+    monkeypatch.setenv("QW4_DMA", "0")
+    monkeypatch.setenv("QW4_ROWS", "2")
+    monkeypatch.setenv("QW4_ROWS_W", "8")
+    want = run()
+    monkeypatch.delenv("QW4_ROWS")
+    monkeypatch.delenv("QW4_ROWS_W")
+    for depth in ("2", "3", "4", None):
+        if depth is None:
+            monkeypatch.delenv("QW4_DMA")   # the default depth
+        else:
+            monkeypatch.setenv("QW4_DMA", depth)
+        got = run()
+        assert np.array_equal(got, want), depth
+
+
+# the model's projections, one group (G < waves), an odd group count, few units
+# and the 8-way shards
+SHAPES = [(7168, 5120), (5120, 4096), (34816, 5120), (5120, 17408), (64, 128), (192, 384),
+          (640, 1280), (896, 5120), (4352, 5120), (5120, 512), (5120, 2176)]
+
+
+@pytest.mark.parametrize("N,K", SHAPES)
+def test_dma_gemv(hip, scratch, monkeypatch, N, K):
+    w, x = _gen(hip, N, K, seed=N + K), _x(hip, K, 7000 + K)
+    print(f"dma gemv {N}x{K}", flush=True)
+
+    def bf16():
+        y = empty((1, N), np.uint16)
+        hip.gemv_w4a16(y, w, x, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def f32():
+        y = empty((1, N), np.float32)
+        hip.gemv_w4a16_f32(y, w, x, scratch)
+        _sync()
+        return host(y, np.float32)
+
+    _both(monkeypatch, bf16)
+    _both(monkeypatch, f32)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 4096), (5120, 17408), (320, 640)])
+def test_dma_residual(hip, scratch, monkeypatch, N, K):
+    w, x, h0 = _gen(hip, N, K, seed=N), _x(hip, K, 11), _x(hip, N, 12)
+    print(f"dma residual {N}x{K}", flush=True)
+
+    def run():
+        h = h0.clone()
+        hip.gemv_residual_w4a16(h, w, x, 1, scratch)
+        _sync()
+        return host(h, np.uint16)
+
+    _both(monkeypatch, run)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("N,K", [(34816, 5120), (256, 640), (4352, 5120)])
+def test_dma_swiglu(hip, scratch, monkeypatch, N, K):
+    w, x = _gen(hip, N, K, seed=N + 1), _x(hip, K, 13)
+    print(f"dma swiglu {N}x{K}", flush=True)
+
+    def run():
+        y = empty((1, N // 2), np.uint16)
+        hip.gemv_swiglu_w4a16(y, w, x, 1, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    _both(monkeypatch, run)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("N,K", [(7168, 5120), (896, 5120), (128, 256)])
+def test_dma_rmsnorm(hip, scratch, monkeypatch, N, K):
+    import torch
+
+    w, h = _gen(hip, N, K, seed=N + 2), _x(hip, K, 14)
+    nw = _x(hip, K, 15)
+    nw.copy_((nw.view(torch.bfloat16) * 0.1).view(torch.int16))
+    print(f"dma rmsnorm {N}x{K}", flush=True)
+
+    def run():
+        y = empty((1, N), np.uint16)
+        hip.gemv_rmsnorm_w4a16(y, w, h, nw, 1e-6, 1, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    _both(monkeypatch, run)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("N", [248320, 4096, 64])
+def test_dma_argmax(hip, scratch, monkeypatch, N):
+    K = 5120
+    w, x = _gen(hip, N, K, seed=N + 3), _x(hip, K, 16)
+    print(f"dma argmax {N}", flush=True)
+
+    def run():
+        idx = empty((1,), np.int32)
+        hip.gemv_argmax_w4a16(idx, w, x, 1, scratch)
+        _sync()
+        return host(idx, np.int32)
+
+    _both(monkeypatch, run)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("N,K", [(31040, 5120), (640, 1280)])
+def test_dma_w8(hip, scratch, monkeypatch, N, K):
+    src = _x(hip, N * K, 17)
+    w = hip.quantize_w8a16(src, N, K)
+    x = _x(hip, K, 18)
+    del src
+    print(f"dma w8 {N}x{K}", flush=True)
+
+    def bf16():
+        y = empty((1, N), np.uint16)
+        hip.gemv_w8a16(y, w, x, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def argmax():
+        idx = empty((1,), np.int32)
+        hip.gemv_argmax_w8a16(idx, w, x, 1, scratch)
+        _sync()
+        return host(idx, np.int32)
+
+    _both(monkeypatch, bf16)
+    _both(monkeypatch, argmax)
+    hip.w8a16_free(w)
+
+
+@pytest.mark.parametrize("N,K", [(5120, 4096), (1024, 2048), (64, 128)])
+def test_dma_vs_oracle(hip, orc, scratch, monkeypatch, N, K):
+    monkeypatch.delenv("QW4_DMA", raising=False)
+    q, zp, s = orc.gen_weights(N, K, seed=N + 1)
+    x = orc.gen_x(1, K, seed=1)
+    w = repack_from_logical(hip, orc, q, zp, s)
+    y = empty((1, N), np.uint16)
+    hip.gemv_w4a16(y, w, dev(x), scratch)
+    _sync()
+    m = orc.parity_metrics(host(y, np.uint16), orc.matmul_f64(x, q, zp, s))
+    print(f"dma oracle {N}x{K}: {m}", flush=True)
+    assert m["max_rel"] <= 1e-2 and m["mean_abs_vs_bf16_ref"] <= 1e-3, m
+    hip.awq_free(w)
