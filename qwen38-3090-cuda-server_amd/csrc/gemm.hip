@@ -59,7 +59,9 @@ struct GemmArgs {
   uint16_t* C;
   float* slots;         // stream-K: [P][2] fp32 partial tiles
   int M, N, K, G, tiles_n, tiles_m, map;
-  int P, U;             // workgroups, (tile, group) units
+  int P;                // workgroups
+  int full;             // tiles [0, full) are done whole, P at a time
+  int U;                // (tile, group) units of tiles [full, tiles), split over P
 };
 
 // NH = 1: a wave owns one 32-row tile half against all 8 m-blocks;
@@ -292,6 +294,7 @@ __device__ __forceinline__ void g2_slot_store(__amdgpu_buffer_rsrc_t rs,
     }
 }
 
+// Ranges over the split tiles' units (unit u: tile full + u / G).
 __device__ __forceinline__ int g2_range_start(const GemmArgs& a, int vp) {
   return (int)((long long)vp * a.U / a.P);
 }
@@ -305,8 +308,9 @@ __device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
 template <int NH>
 __global__ __launch_bounds__(512) void k_gemm_fixup(GemmArgs a) {
   constexpr int MBW = G2_MB / NH;
-  const int t = blockIdx.x;
-  const int p0 = g2_owner_of(a, t * a.G), p1 = g2_owner_of(a, t * a.G + a.G - 1);
+  const int ts = blockIdx.x;   // split tile full + ts
+  const int t = a.full + ts;
+  const int p0 = g2_owner_of(a, ts * a.G), p1 = g2_owner_of(a, ts * a.G + a.G - 1);
   if (p0 == p1) return;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -325,7 +329,7 @@ __global__ __launch_bounds__(512) void k_gemm_fixup(GemmArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) acc[j][mb] = f32x16v{};
   for (int pp = p0; pp <= p1; ++pp) {
-    const int which = (g2_range_start(a, pp) / a.G == t) ? 0 : 1;
+    const int which = (g2_range_start(a, pp) / a.G == ts) ? 0 : 1;
 #pragma unroll
     for (int j = 0; j < NH; ++j)
 #pragma unroll
@@ -354,10 +358,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
   const NibConst kc = nib_const();
   f32x16v acc[NH][MBW];
 
-  // Virtual workgroup vp owns units [start(vp), start(vp + 1)) of the
-  // U = tiles x G (tile, group) units; XCD x owns a contiguous run of vp. With
-  // P = tiles (U / P = G) every range is exactly one whole tile; with P = CUs
-  // ranges cut tiles (stream-K) and the cut tiles are combined through slots.
+  // Virtual workgroup vp (XCD x owns a contiguous run of vp) first does the
+  // whole tiles vp, vp + P, ... < full, then the units [start(vp),
+  // start(vp + 1)) of the U = (tiles - full) x G units of the remaining
+  // tiles: ranges that cut a tile (stream-K) are combined through slots.
+  // P = tiles, full = tiles: one whole tile per workgroup.
   const int vp = a.map ? g2_xcd_order(blockIdx.x, a.P) : (int)blockIdx.x;
   const int u0 = g2_range_start(a, vp), u1 = g2_range_start(a, vp + 1);
   const __amdgpu_buffer_rsrc_t rs =
@@ -369,11 +374,20 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
                                             (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
   wr.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
                                             (int)((uint32_t)a.N * (uint32_t)a.G / 2u), 0x00020000);
-  for (int u = u0; u < u1;) {
-    const int t = u / a.G, g0 = u - t * a.G;
-    const int g1 = min(a.G, u1 - t * a.G);
+  for (int t = vp; t < a.full; t += a.P) {
     int tn, tm;
     g2_tile_coords(a, t, tn, tm);
+    const int tile = tn * 4 + wt;
+    const bool valid = tile * kTileN < a.N;
+    const int ltile = valid ? tile : (a.N / kTileN - 1);
+    g2_segment<NH>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane, kc);
+    if (valid) g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+  }
+  for (int u = u0; u < u1;) {
+    const int ts = u / a.G, g0 = u - ts * a.G;
+    const int g1 = min(a.G, u1 - ts * a.G);
+    int tn, tm;
+    g2_tile_coords(a, a.full + ts, tn, tm);
     const int tile = tn * 4 + wt;
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
@@ -383,7 +397,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
     } else {
       g2_slot_store<NH>(rs, acc, vp, u == u0 ? 0 : 1, wave, lane);
     }
-    u = t * a.G + g1;
+    u = ts * a.G + g1;
   }
 }
 
@@ -451,27 +465,46 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     }();
     const int nt = tiles_n * tiles_m;
     GemmArgs a{w->qweight, w->scale, w->zeros, A, C, nullptr, M, w->out_f, w->in_f,
-                w->num_groups, tiles_n, tiles_m, map_env && nt % 8 == 0, nt, nt * w->num_groups};
+                w->num_groups, tiles_n, tiles_m, map_env && nt % 8 == 0, nt, nt, 0};
     int grid = nt;
-    // Stream-K (one workgroup per CU, the (tile, group) units split evenly)
-    // when it beats one workgroup per tile by a margin. Costs in group-steps
-    // per CU: whole tiles take ceil(nt / CUs) * G; stream-K takes nt * G / CUs
-    // plus ~16 for writing and re-reading the cut tiles' fp32 partials.
-    static const int sk_env = [] {
-      const char* e = std::getenv("QW4_GEMM_SK");
-      return e ? std::atoi(e) : -1;   // -1: by the cost model, 0: never, 1: always
-    }();
+    // Three schedules, costed in group-steps per CU (one 256 x 256 x 128
+    // tile step; measured on MI355X at the config-4 shapes):
+    //  * per tile: one workgroup per tile, ceil(nt / CUs) G;
+    //  * stream-K: one workgroup per CU, all nt G (tile, group) units split
+    //    evenly, nt G / CUs + 16 (two fp32 partial tiles written per
+    //    workgroup) + 0.75 per piece of a cut tile (k_gemm_fixup reads the
+    //    pieces of a tile one after another);
+    //  * hybrid: whole tiles for the floor(nt / CUs) full rounds, then the
+    //    other nt % CUs tiles split over the CUs: the same work, one partial
+    //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile.
+    // A split schedule runs when it beats per-tile by 10%. QW4_GEMM_SK: 0
+    // never splits, 1 forces stream-K, 2 the hybrid (read on every call).
+    const char* ske = std::getenv("QW4_GEMM_SK");
+    const int sk_env = ske ? std::atoi(ske) : -1;
     const int cus = device_cus();
     const long long G = w->num_groups;
+    const int rem = nt % cus;
     const double t_dp = (double)((nt + cus - 1) / cus) * G;
-    const double t_sk = (double)nt * G / cus + 16.0;
-    const bool sk_ok = ws && ws->buf && ws->bytes >= gemm_workspace_need(cus) &&
-                       cus % 8 == 0 && nt % cus != 0 && (long long)nt * G >= 2LL * cus &&
-                       (long long)nt * G < (1LL << 31);
-    if (sk_ok && (sk_env == 1 || (sk_env == -1 && t_sk < 0.9 * t_dp))) {
+    const double work = (double)nt * G / cus;
+    const double t_sk = work + 16.0 + 0.75 * ((cus + nt - 1) / nt + 1);
+    const double t_hy = work + 8.0 + 0.75 * (rem ? (cus + rem - 1) / rem + 1 : 0);
+    const bool ws_ok = ws && ws->buf && ws->bytes >= gemm_workspace_need(cus) && cus % 8 == 0 &&
+                       rem != 0 && (long long)nt * G < (1LL << 31);
+    const bool sk_ok = ws_ok && (long long)nt * G >= 2LL * cus;
+    const bool hy_ok = ws_ok && nt > cus && (long long)rem * G >= (long long)cus;
+    int pick = 0;   // 0 per tile, 1 stream-K, 2 hybrid
+    if (sk_env == 1 && sk_ok) pick = 1;
+    else if (sk_env == 2 && hy_ok) pick = 2;
+    else if (sk_env == -1) {
+      double best = 0.9 * t_dp;
+      if (sk_ok && t_sk < best) { pick = 1; best = t_sk; }
+      if (hy_ok && t_hy < best) pick = 2;
+    }
+    if (pick) {
       a.slots = static_cast<float*>(ws->buf);
       a.P = cus;
-      a.U = (int)(nt * G);
+      a.full = pick == 2 ? nt - rem : 0;
+      a.U = (int)((nt - a.full) * G);
       a.map = 1;
       grid = cus;
     }
@@ -483,9 +516,9 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     if (nh == 2) k_gemm<2><<<grid, 512, 0, s>>>(a);
     else k_gemm<1><<<grid, 512, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
-    if (grid != nt) {
-      if (nh == 2) k_gemm_fixup<2><<<nt, 512, 0, s>>>(a);
-      else k_gemm_fixup<1><<<nt, 512, 0, s>>>(a);
+    if (a.full != nt) {   // the split tiles
+      if (nh == 2) k_gemm_fixup<2><<<nt - a.full, 512, 0, s>>>(a);
+      else k_gemm_fixup<1><<<nt - a.full, 512, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;

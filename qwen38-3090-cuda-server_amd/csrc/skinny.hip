@@ -874,7 +874,7 @@ __device__ __forceinline__ void emit_swiglu(const SkinnyArgs& a, int b, int st0,
 template <int OUT, int FMT, int S, int W, bool XL, int D, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   static_assert(!DMA || XL, "LDS-DMA items need the staged activations");
-  constexpr int kPer = 4 / S;   // units per tile
+  constexpr uint32_t kPer = 4 / S;   // units per tile (unit indices are never negative)
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
   constexpr int kRedLanes = DMA ? 16 : 64;
   constexpr int kXC = rows_xchunks(DMA);
@@ -895,7 +895,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   const int u1 =
       OUT == OUT_SWIGLU ? 2 * (int)((long long)(p + 1) * (a.U / 2) / a.P) : range_start(a, p + 1);
   auto real_unit = [&](int v) {
-    return OUT == OUT_SWIGLU ? ((v & 1) ? (v >> 1) + a.U / 2 : (v >> 1)) : v;
+    return OUT == OUT_SWIGLU ? ((v & 1) ? (v >> 1) + (int)((uint32_t)a.U / 2u) : (v >> 1)) : v;
   };
   const NibConst k = nib_const();
   Best bs;
@@ -908,7 +908,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   auto load_next = [&](RowsData<FMT, S, XL>& d) {
     const bool in = lu < u1;
     const int ru = real_unit(lu);
-    const int b = in ? ru / kPer : 0, st0 = in ? (ru % kPer) * S : 0;
+    const int b = in ? (int)((uint32_t)ru / kPer) : 0;
+    const int st0 = in ? (int)((uint32_t)ru % kPer) * S : 0;
     const int g = in ? lg : 0;
     rows_load<FMT, S, XL>(d, rs, in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk, g,
                           wbase + (uint32_t)st0 * kQuad, (uint32_t)(4 * c + st0) * 2u, zoff,
@@ -925,7 +926,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   auto load_slot = [&](int j) {
     const bool in = lu < u1;
     const int ru = real_unit(lu);
-    const int b = in ? ru / kPer : 0, st0 = in ? (ru % kPer) * S : 0;
+    const int b = in ? (int)((uint32_t)ru / kPer) : 0;
+    const int st0 = in ? (int)((uint32_t)ru % kPer) * S : 0;
     const int g = in ? lg : 0;
     dma_issue<FMT, S>(ring + j * DmaSlot<FMT, S>::kUnits, rs,
                       in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk,
@@ -1036,10 +1038,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
           f32x4 g[S];
 #pragma unroll
           for (int i = 0; i < S; ++i) g[i] = gate[i & (OUT == OUT_SWIGLU ? 0xff : 0)];
-          emit_swiglu<S>(a, gu / kPer, (gu % kPer) * S, g, t, lane);
+          emit_swiglu<S>(a, (int)((uint32_t)gu / kPer), (int)((uint32_t)gu % kPer) * S, g, t,
+                         lane);
         }
       } else {
-        emit_rows<OUT, S>(a, closed / kPer, (closed % kPer) * S, t, lane, bs);
+        emit_rows<OUT, S>(a, (int)((uint32_t)closed / kPer), (int)((uint32_t)closed % kPer) * S, t,
+                          lane, bs);
       }
     }
     par ^= 1;
@@ -1050,7 +1054,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
 
   int cg = wave;   // compute cursor: unit `closed`, group cg
   auto step = [&](RowsData<FMT, S, XL>& d, bool reload) {
-    rows_mma<FMT, S, XL>(acc, d, k, (real_unit(closed) % kPer) * S, zsh, xrow + cg * 16);
+    rows_mma<FMT, S, XL>(acc, d, k, (int)((uint32_t)real_unit(closed) % kPer) * S, zsh,
+                         xrow + cg * 16);
     if (reload) load_next(d);
     cg += W;
     if (cg >= a.G) {
@@ -1069,7 +1074,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     auto step_dma = [&](auto jc, auto nc, bool reload) {
       constexpr int j = decltype(jc)::value;
       wait_vm<decltype(nc)::value>();
-      const int st0 = (real_unit(closed) % kPer) * S;
+      const int st0 = (int)((uint32_t)real_unit(closed) % kPer) * S;
       RowsData<FMT, S, XL> d;
       dma_read<FMT, S, XL>(d, ring + j * DmaSlot<FMT, S>::kUnits, lane, st0);
       rows_mma<FMT, S, XL, 1>(acc, d, k, st0, zsh, xrow + cg * 16);
@@ -1267,10 +1272,11 @@ Launch launch_for(int out_f, int G, int M) {
   l.P = (int)std::max<long long>(1, std::min(cap, (U + l.W - 1) / l.W));
   l.S = 0;
   // Data-parallel k_rows (no cross-workgroup exchange) by default. Unit size
-  // and waves measured on MI355X over the model's projections and the head:
-  // S = 2 (32-row units) when the output has fewer 64-row tiles than CUs,
-  // else S = 4; M = 1: 16 waves for K >= 64 groups, else 8; M > 1 and the
-  // argmax: 8 waves. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces S (read
+  // and waves measured on MI355X over the model's projections, their 8-way
+  // shards and the head: S = 1 (16-row units) when the output has fewer
+  // 64-row tiles than CUs / 4 (a 896-row shard: 4.7 vs 5.6 us), S = 2
+  // (32-row units) when it has fewer tiles than CUs, else S = 4; M = 1:
+  // 16 waves for K >= 64 groups, else 8; M > 1 and the argmax: 8 waves. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces S (read
   // on every call); QW4_ROWS_W forces the waves.
   const char* er = std::getenv("QW4_ROWS");
   const int env_rows = er ? std::atoi(er) : -1;
@@ -1281,8 +1287,9 @@ Launch launch_for(int out_f, int G, int M) {
   // OUT_SWIGLU pairs a gate unit with its up unit in one workgroup: 32-row
   // units keep as many workgroups as the plain GEMV's 64-row units
   l.S = (env_rows == 1 || env_rows == 2 || env_rows == 4) ? env_rows
-        : (OUT == OUT_SWIGLU || tiles < device_cus()) ? 2
-                                                      : 4;
+        : (OUT != OUT_SWIGLU && 4 * tiles < device_cus()) ? 1
+        : (OUT == OUT_SWIGLU || tiles < device_cus())     ? 2
+                                                          : 4;
   if (OUT == OUT_ARGMAX)
     l.W = 8;   // the running argmax does not fit 16 waves' registers
   else if (env_rows_w == 8 || env_rows_w == 16)
@@ -1318,9 +1325,10 @@ Launch launch_for(int out_f, int G, int M) {
   // epilogues gain up to 8%, while the fused rmsnorm and the 8-bit head run
   // faster with register items, which stay their default. QW4_DMA = 0 keeps
   // register items, 2 | 3 | 4 forces LDS-DMA items of that depth for every
-  // mode (read on every call); QW4_ROWS / QW4_ROWS_W other than 2 / 8 keep
-  // register items.
-  if (M == 1 && (env_rows < 0 || env_rows == 2) && (env_rows_w == 0 || env_rows_w == 8)) {
+  // mode (read on every call); 16-row units and QW4_ROWS / QW4_ROWS_W other
+  // than 2 / 8 keep register items.
+  if (M == 1 && (env_rows == 2 || (env_rows < 0 && l.S != 1)) &&
+      (env_rows_w == 0 || env_rows_w == 8)) {
     const char* ed = std::getenv("QW4_DMA");
     const int dd = ed ? std::atoi(ed)
                    : (OUT == OUT_NORM || FMT == 8) ? 0

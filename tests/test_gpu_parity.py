@@ -244,15 +244,18 @@ def gemm_ws(hip):
 
 @pytest.mark.parametrize("M,N,K", [(1, 128, 512), (77, 320, 1024), (512, 17408, 5120),
                                    (512, 5120, 17408), (200, 5184, 1536), (777, 5184, 4096),
-                                   (300, 5120, 2176), (64, 896, 640)])
+                                   (300, 5120, 2176), (64, 896, 640),
+                                   # 340 tiles: 256 whole, 84 split over the CUs
+                                   (1100, 17408, 5120)])
 @pytest.mark.parametrize("use_ws", [False, True])
 def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     """BASELINE config 4 semantics: RNE(bf16) dequant, fp32 accumulation, bf16 out.
     The oracle is evaluated on a sample of rows of A (each output row depends only
     on its own row of A). With a workspace, shapes whose tiles do not fill the
     chip evenly run stream-K (tiles cut across workgroups, partials combined in
-    a fixed order): checked against the oracle and bitwise against the
-    one-workgroup-per-tile result."""
+    a fixed order): checked against the oracle and bitwise against a
+    second run (reproducibility). Past one full round of tiles the hybrid
+    schedule does whole tiles first and splits only the remaining ones."""
     import torch
 
     q, zp, s = orc.gen_weights(N, K, seed=M)
