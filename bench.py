@@ -339,6 +339,7 @@ class Bench:
         hip.w8a16_free(w8)
         log(f"config5 w8: {c5w8}")
         self.layer_steps()
+        self.reference_mix()
 
     # ------------------------------------------- fused steps around the GEMVs
     def layer_steps(self):
@@ -380,6 +381,49 @@ class Bench:
             out[name] = {"separate_us": per_layer(sep), "fused_us": per_layer(fus)}
         self.extra["layer_steps_m1"] = out
         log(f"layer steps: {out}")
+
+    def reference_mix(self):
+        """The reference's own decode-GEMV benchmark mix (bench/bench_decode_gemv.cu:
+        88-98, fused): per token 48 GatedDeltaNet layers (in_proj qkv|z
+        5120->16384, out_proj 6144->5120), 16 attention layers (q|k|v
+        5120->14336, o_proj 6144->5120) and 64 MLPs (gate|up, down), M = 1. It
+        reports the traffic-weighted aggregate against its measured DRAM read
+        bandwidth (84.2% on its GPU); here per-op graphs over 24 distinct copies
+        (gate|up and down: the sweep's 64 layers), algorithmic bytes."""
+        hip, torch, scratch = self.hip, self.torch, self.scratch
+        ops = [("gdn.in_proj_qkv|z", 5120, 16384, 48), ("gdn.out_proj", 6144, 5120, 48),
+               ("attn.q|k|v", 5120, 14336, 16), ("attn.o_proj", 6144, 5120, 16)]
+        x6 = torch.empty(6144, dtype=torch.int16, device="cuda")
+        hip.gen_bf16(x6, 6144, 0, 6144, 0)
+        xs = {5120: self.xs[5120], 17408: self.xs[17408], 6144: x6}
+        y = torch.empty(16384, dtype=torch.int16, device="cuda")
+        out, tb, tt = {}, 0.0, 0.0
+        for i, (name, K, N, reps) in enumerate(ops):
+            ws = [self.weights(N, K, 5000 + 32 * i + c) for c in range(24)]
+            g = self.capture(lambda: [hip.gemv_w4a16(y, w, xs[K], scratch) for w in ws])
+            us = self.time_graph(g, 3) / len(ws) * 1e3
+            del g
+            for w in ws:
+                hip.awq_free(w)
+            b = alg_bytes(1, K, N)
+            out[name] = {"K": K, "N": N, "per_token": reps, "us": round(us, 2),
+                         "GBps": round(b / (us * 1e-6) / 1e9, 1)}
+            tb += b * reps
+            tt += us * reps
+        for name, K, N in (("mlp.gate|up", 5120, 34816), ("mlp.down", 17408, 5120)):
+            us = self.extra["config2_per_projection"]["gate|up" if "gate" in name else "down"]["us"]
+            b = alg_bytes(1, K, N)
+            out[name] = {"K": K, "N": N, "per_token": 64, "us": us,
+                         "GBps": round(b / (us * 1e-6) / 1e9, 1)}
+            tb += b * 64
+            tt += us * 64
+        agg = tb / (tt * 1e-6) / 1e9
+        hbm = self.extra.get("measured_hbm_read_GBps")
+        self.extra["reference_mix_m1"] = {
+            "ops": out, "weight_GiB_per_token": round(tb / 2 ** 30, 3),
+            "ms_per_token": round(tt / 1e3, 3), "GBps": round(agg, 1),
+            "frac_of_measured_hbm": round(agg / hbm, 4) if hbm else None}
+        log(f"reference mix: {agg:.1f} GB/s, {tt / 1e3:.3f} ms/token")
 
     # ---------------------------------------------------------- config 4
     def prefill(self):
