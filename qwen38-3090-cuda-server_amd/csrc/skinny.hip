@@ -867,16 +867,18 @@ __device__ __forceinline__ void emit_swiglu(const SkinnyArgs& a, int b, int st0,
 // and passes one barrier, so the waves stay in step for any G; wave 0 then
 // sums the W partials in wave order and emits the unit. No workgroup depends
 // on another.
-// DMA (with XL, M = 1): items are loaded into LDS slots (DmaSlot) instead of
-// registers, D per wave after the staged activations; the one output row sits
-// in lanes 0..15 (element jj = 0), so only those lanes take part in the unit
-// sums and only that element is accumulated.
+// DMA: items' weights and metadata are loaded into LDS slots (DmaSlot)
+// instead of registers, D per wave after the staged activations (if any).
+// With XL (M = 1) the one output row sits in lanes 0..15 (element jj = 0), so
+// only those lanes take part in the unit sums and only that element is
+// accumulated; without (M > 1) each item's activations still go to registers,
+// loaded with the item.
 template <int OUT, int FMT, int S, int W, bool XL, int D, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
-  static_assert(!DMA || XL, "LDS-DMA items need the staged activations");
+  constexpr bool kM1 = DMA && XL;   // LDS-DMA items with staged activations: M = 1
   constexpr uint32_t kPer = 4 / S;   // units per tile (unit indices are never negative)
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
-  constexpr int kRedLanes = DMA ? 16 : 64;
+  constexpr int kRedLanes = kM1 ? 16 : 64;
   constexpr int kXC = rows_xchunks(DMA);
   __shared__ f32x4 red[2][W][S][kRedLanes];
   extern __shared__ u32x4 xlds[];
@@ -921,9 +923,9 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     }
   };
 
-  RowsData<FMT, S, XL> buf[DMA ? 1 : D];
-  u32x4* const ring = xlds + a.M * a.K / 8 + wave * D * DmaSlot<FMT, S>::kUnits;
-  auto load_slot = [&](int j) {
+  RowsData<FMT, S, XL> buf[kM1 ? 1 : D];
+  u32x4* const ring = xlds + (XL ? a.M * a.K / 8 : 0) + wave * D * DmaSlot<FMT, S>::kUnits;
+  auto load_slot = [&](int j) __attribute__((always_inline)) {
     const bool in = lu < u1;
     const int ru = real_unit(lu);
     const int b = in ? (int)((uint32_t)ru / kPer) : 0;
@@ -932,6 +934,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     dma_issue<FMT, S>(ring + j * DmaSlot<FMT, S>::kUnits, rs,
                       in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk,
                       wbase + (uint32_t)st0 * kQuad, lane);
+    if (!XL) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        buf[j & (kM1 ? 0 : 0xff)].x[t & (XL ? 0 : 3)] =
+            __builtin_amdgcn_raw_buffer_load_b128(rs.x, xoff + t * 16, (uint32_t)g * 256u, 0);
+    }
     lg += W;
     if (lg >= a.G) {
       lg = wave;
@@ -1016,7 +1024,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   int par = 0, closed = u0;
   f32x4 gate[OUT == OUT_SWIGLU ? S : 1];   // OUT_SWIGLU: the gate unit's sums (wave 0)
   auto close_unit = [&]() {
-    if (!DMA || lane < kRedLanes) {
+    if (!kM1 || lane < kRedLanes) {
 #pragma unroll
       for (int i = 0; i < S; ++i) red[par][wave][i][lane % kRedLanes] = acc[i];
     }
@@ -1070,14 +1078,18 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   if constexpr (DMA) {
     // item t waits for its slot; the loads of the items after it (all D - 1
     // of them in the main loop, fewer in the tail) may still be in flight
-    constexpr int kL = DmaSlot<FMT, S>::kLoads;
-    auto step_dma = [&](auto jc, auto nc, bool reload) {
+    constexpr int kL = DmaSlot<FMT, S>::kLoads + (XL ? 0 : 4);
+    auto step_dma = [&](auto jc, auto nc, bool reload) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value;
       wait_vm<decltype(nc)::value>();
       const int st0 = (int)((uint32_t)real_unit(closed) % kPer) * S;
       RowsData<FMT, S, XL> d;
       dma_read<FMT, S, XL>(d, ring + j * DmaSlot<FMT, S>::kUnits, lane, st0);
-      rows_mma<FMT, S, XL, 1>(acc, d, k, st0, zsh, xrow + cg * 16);
+      if constexpr (!XL) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d.x[t & (XL ? 0 : 3)] = buf[j & (kM1 ? 0 : 0xff)].x[t & (XL ? 0 : 3)];
+      }
+      rows_mma<FMT, S, XL, kM1 ? 1 : 4>(acc, d, k, st0, zsh, xrow + cg * 16);
       if (reload) {
         // the slot's LDS reads have returned before it is loaded again
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -1344,6 +1356,30 @@ Launch launch_for(int out_f, int G, int M) {
       const long long pc2 = (long long)device_cus() * (kLdsBytes / need);
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, pc2));
     }
+  } else if (M > 1 && OUT != OUT_NORM && l.S != 1 && (env_rows_w == 0 || env_rows_w == 8)) {
+    // M > 1: LDS-DMA weight items, activations loaded with each item, units
+    // of the register policy's size (64 rows when the output has at least as
+    // many tiles as CUs: each activation load then serves 4 row quads).
+    // Measured on MI355X (verify M = 9 / 16 over the model's projections): 2
+    // items per wave beat register items by 3% / 5% per layer (down M = 16:
+    // 10%); deeper is slower. QW4_DMA = 2 | 3 | 4 forces the depth, 0 keeps
+    // register items.
+    const char* ed = std::getenv("QW4_DMA");
+    const int S = l.S;
+    // (64-row units: the argmax keeps its running maxima in registers and
+    // spills past 2 items)
+    const int dd = std::min(ed ? std::atoi(ed) : 2,
+                            (OUT == OUT_ARGMAX && S == 4) ? 2 : 4);
+    const int slot = (FMT == 8 ? 2 * S : S) * 1024 + (FMT == 4 ? 512 : 256);
+    const int need = 8 * dd * slot + 2 * 8 * S * 64 * 16;
+    if (dd >= 2 && dd <= 4 && need <= kLdsBytes) {
+      l.DMA = dd;
+      l.W = 8;
+      l.XL = false;
+      const long long us = (long long)tiles * 4 / S;
+      const long long pc2 = (long long)device_cus() * (kLdsBytes / need);
+      l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? us / 2 : us, pc2));
+    }
   }
   return l;
 }
@@ -1371,29 +1407,41 @@ void allow_lds(K kern, int bytes) {
   }
 }
 
-template <int OUT, int FMT, int S, int W, int D>
+template <int OUT, int FMT, int S, int W, int D, bool XL>
 void launch_rows_dma_d(const SkinnyArgs& a, hipStream_t st) {
-  const int lds = a.M * a.K * 2 + W * D * DmaSlot<FMT, S>::kUnits * 16;
-  auto kern = k_rows<OUT, FMT, S, W, true, D, true>;
+  const int lds = (XL ? a.M * a.K * 2 : 0) + W * D * DmaSlot<FMT, S>::kUnits * 16;
+  auto kern = k_rows<OUT, FMT, S, W, XL, D, true>;
   allow_lds(kern, lds);
   kern<<<a.P, 64 * W, lds, st>>>(a);
 }
 
-// M = 1 with LDS-DMA items: 32-row units, 8 waves, D items per wave
-template <int OUT, int FMT>
+// LDS-DMA items: units of S row quads, 8 waves, D items per wave; staged
+// activations (M = 1, S = 2) or activations loaded with each item (M > 1)
+template <int OUT, int FMT, int S, bool XL>
 void launch_rows_dma(const SkinnyArgs& a, int D, hipStream_t st) {
-  if (D == 2)
-    launch_rows_dma_d<OUT, FMT, 2, 8, 2>(a, st);
-  else if (D == 3)
-    launch_rows_dma_d<OUT, FMT, 2, 8, 3>(a, st);
-  else
-    launch_rows_dma_d<OUT, FMT, 2, 8, 4>(a, st);
+  if constexpr (OUT == OUT_ARGMAX && S == 4) {   // deeper would spill (launch_for caps D)
+    launch_rows_dma_d<OUT, FMT, S, 8, 2, XL>(a, st);
+  } else {
+    if (D == 2)
+      launch_rows_dma_d<OUT, FMT, S, 8, 2, XL>(a, st);
+    else if (D == 3)
+      launch_rows_dma_d<OUT, FMT, S, 8, 3, XL>(a, st);
+    else
+      launch_rows_dma_d<OUT, FMT, S, 8, 4, XL>(a, st);
+  }
 }
 
 template <int OUT, int FMT>
 void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
   if (l.DMA) {
-    launch_rows_dma<OUT, FMT>(a, l.DMA, st);
+    if (l.XL)
+      launch_rows_dma<OUT, FMT, 2, true>(a, l.DMA, st);
+    else if constexpr (OUT != OUT_NORM) {
+      if (l.S == 4)
+        launch_rows_dma<OUT, FMT, 4, false>(a, l.DMA, st);
+      else
+        launch_rows_dma<OUT, FMT, 2, false>(a, l.DMA, st);
+    }
     return;
   }
   if (OUT == OUT_ARGMAX || l.W == 8)

@@ -216,3 +216,90 @@ def test_dma_vs_oracle(hip, orc, scratch, monkeypatch, N, K):
     print(f"dma oracle {N}x{K}: {m}", flush=True)
     assert m["max_rel"] <= 1e-2 and m["mean_abs_vs_bf16_ref"] <= 1e-3, m
     hip.awq_free(w)
+
+
+# ------------------------------------------------- M > 1 (verify, heads)
+def _both_m(monkeypatch, run, rows="2"):
+    """M > 1: LDS-DMA weight items (activations loaded with each item) against
+    register items, 8 waves, 32-row units (rows="2") or the policy's unit size
+    (rows=None: 64-row units for outputs with at least as many tiles as CUs)."""
+    monkeypatch.setenv("QW4_DMA", "0")
+    if rows:
+        monkeypatch.setenv("QW4_ROWS", rows)
+    else:
+        monkeypatch.delenv("QW4_ROWS", raising=False)
+    monkeypatch.setenv("QW4_ROWS_W", "8")
+    want = run()
+    for depth in ("2", "3", "4", None):
+        if depth is None:
+            monkeypatch.delenv("QW4_DMA")   # the default for this shape
+        else:
+            monkeypatch.setenv("QW4_DMA", depth)
+        got = run()
+        assert np.array_equal(got, want), depth
+
+
+@pytest.mark.parametrize("M", [2, 9, 16])
+@pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 17408), (192, 384), (34816, 5120)])
+def test_dma_verify(hip, scratch, monkeypatch, N, K, M):
+    w = _gen(hip, N, K, seed=N + K + M)
+    x, h0 = _x(hip, M * K, 20 + M), _x(hip, M * N, 30 + M)
+    print(f"dma verify M={M} {N}x{K}", flush=True)
+
+    def gemm():
+        y = empty((M, N), np.uint16)
+        hip.gemm_small_w4a16(y, w, x, M, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def residual():
+        h = h0.clone()
+        hip.gemv_residual_w4a16(h, w, x, M, scratch)
+        _sync()
+        return host(h, np.uint16)
+
+    def argmax():
+        idx = empty((M,), np.int32)
+        hip.gemv_argmax_w4a16(idx, w, x, M, scratch)
+        _sync()
+        return host(idx, np.int32)
+
+    for rows in ("2", None):
+        _both_m(monkeypatch, gemm, rows)
+        _both_m(monkeypatch, residual, rows)
+        _both_m(monkeypatch, argmax, rows)
+    if M == 2 and N % 128 == 0:
+        def swiglu():
+            y = empty((M, N // 2), np.uint16)
+            hip.gemv_swiglu_w4a16(y, w, x, M, scratch)
+            _sync()
+            return host(y, np.uint16)
+
+        _both_m(monkeypatch, swiglu)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("M", [2, 9])
+def test_dma_w8_verify(hip, scratch, monkeypatch, M):
+    N, K = 31040, 5120
+    src = _x(hip, N * K, 19)
+    w = hip.quantize_w8a16(src, N, K)
+    x = _x(hip, M * K, 21)
+    del src
+
+    def gemm():
+        y = empty((M, N), np.uint16)
+        hip.gemm_small_w8a16(y, w, x, M, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def argmax():
+        idx = empty((M,), np.int32)
+        hip.gemv_argmax_w8a16(idx, w, x, M, scratch)
+        _sync()
+        return host(idx, np.int32)
+
+    for rows in ("2", None):
+        _both_m(monkeypatch, gemm, rows)
+        _both_m(monkeypatch, argmax, rows)
+    hip.w8a16_free(w)
