@@ -118,15 +118,28 @@ __device__ __forceinline__ void g2_load_act(__amdgpu_buffer_rsrc_t act, const ui
   }
 }
 
-__device__ __forceinline__ bf16x8 g2_deq(uint32_t w, float s, float c, NibConst kc) {
-  const u32x4 m = nib8_bits(w, kc);
+// One packed word -> 8 bf16 weights RNE((q - z) s), c = -z s, in the order
+// of nib8_bits (register i: elements i and i + 4). The even nibbles are the
+// low nibbles of the bytes of w & 0x0F0F0F0F, the odd ones of (w >> 4): each
+// converts to fp32 in one v_cvt_f32_ubyteN, and fma(q, s, -z s) is exact
+// (both products have at most 12 significant bits) -- 23 VALU per word.
+__device__ __forceinline__ bf16x8 g2_deq(uint32_t w, float s, float c) {
+  const uint32_t ev = w & 0x0F0F0F0Fu, od = (w >> 4) & 0x0F0F0F0Fu;
+  float q[8];   // q[2 b] = byte b of ev, q[2 b + 1] = byte b of od
+  asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(q[0]) : "v"(ev));
+  asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(q[2]) : "v"(ev));
+  asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(q[4]) : "v"(ev));
+  asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(q[6]) : "v"(ev));
+  asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(q[1]) : "v"(od));
+  asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(q[3]) : "v"(od));
+  asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(q[5]) : "v"(od));
+  asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(q[7]) : "v"(od));
+  auto f = [&](int e) { return __builtin_fmaf(q[e], s, c); };
   u32x4 o;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float lo = __uint_as_float(m[i] << 16);
-    const float hi = __uint_as_float(m[i] & 0xffff0000u);
-    o[i] = pack_bf16x2(__builtin_fmaf(lo, s, c), __builtin_fmaf(hi, s, c));
-  }
+  o[0] = pack_bf16x2(f(0), f(4));   // elements 0, 4 (bytes 0 and 2 of ev)
+  o[1] = pack_bf16x2(f(1), f(5));   // 1, 5
+  o[2] = pack_bf16x2(f(2), f(6));   // 2, 6
+  o[3] = pack_bf16x2(f(3), f(7));   // 3, 7
   return __builtin_bit_cast(bf16x8, o);
 }
 
@@ -195,7 +208,7 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int j = 0; j < NH; ++j) {
       sf[j] = bf16_bits_to_f32(cur.s[j]);
-      cf[j] = -(128.0f + (float)((cur.z[j] >> zsh) & 0xFu)) * sf[j];
+      cf[j] = -(float)((cur.z[j] >> zsh) & 0xFu) * sf[j];
     }
     // Software pipeline over the group's 8 k-steps: the activation operands
     // and the dequantized weight operands of step u + 1 are produced while
@@ -205,7 +218,7 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) xo[0][mb] = buf[mb * 512 + ((4 * h) ^ (r & 15))];
 #pragma unroll
-    for (int j = 0; j < NH; ++j) wd[0][j] = g2_deq(cur.q[j][0][0], sf[j], cf[j], kc);
+    for (int j = 0; j < NH; ++j) wd[0][j] = g2_deq(cur.q[j][0][0], sf[j], cf[j]);
     // Fence: the prologue's reads must not fill the DS slots of the pattern below.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -217,7 +230,7 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
         for (int mb = 0; mb < MBW; ++mb) xo[nu][mb] = buf[mb * 512 + slot];
 #pragma unroll
-        for (int j = 0; j < NH; ++j) wd[nu][j] = g2_deq(cur.q[j][s1][t1], sf[j], cf[j], kc);
+        for (int j = 0; j < NH; ++j) wd[nu][j] = g2_deq(cur.q[j][s1][t1], sf[j], cf[j]);
       }
 #pragma unroll
       for (int mb = 0; mb < MBW; ++mb)
