@@ -1,48 +1,48 @@
 // Decode GEMV (M = 1), speculative-verify skinny GEMM (M = 2..16) and the
-// lm_head GEMV with a fused fp32 row-argmax, all on one gfx950 kernel.
+// lm_head GEMV with a fused fp32 row-argmax: two gfx950 kernels over the same
+// per-block math.
 //
-// Why stream-K. The path is HBM-bound and the chip streams at most ~10 bytes
-// per clock per CU, so the kernel runs at the speed of its most loaded CU.
-// Giving each workgroup one 64-row tile leaves CUs unevenly loaded (544 tiles on
-// 256 CUs) or idle (80 tiles for a 5120-row projection). Instead the grid is a
-// fixed number of workgroups P sized to the chip, and the flattened list of
-// U = tiles x groups blocks (one 4 KiB (tile, group) block each) is cut into P
-// equal contiguous ranges. A workgroup walks the tiles its range touches; a
-// tile it covers completely it finishes itself, a tile cut by a range boundary
-// ("split tile") is finished by whichever contributor completes it last.
-//
-// Per block, a wave streams 4 KiB with four 16-byte loads per lane (lane
-// c + 16q reads chunk q of positions 16*st + c, i.e. rows 4c + st) and feeds
-// bf16 MFMA v_mfma_f32_16x16x32_bf16:
-//    A = activations, 16 rows (rows >= M read a zero row), 32 k per instruction
+// Math. A 64-row tile of packed weights is split into 4 KiB (tile, group)
+// blocks (4-bit; 8 KiB for 8-bit weights). Lane c + 16q of a wave reads chunk
+// q of positions 16 st + c, i.e. rows 4c + st, and feeds bf16 MFMA
+// v_mfma_f32_16x16x32_bf16:
+//    A = activations, 16 rows (rows >= M unused), 32 k per instruction
 //    B = the packed word turned into 8 bf16 values (128 + q) by AND-OR
 // Four instructions per row quad st cover the group; a fifth B operand of ones
 // gives S_m = sum_k x[m][k] in the same output layout, so the zero-point and
 // +128 correction is
 //    acc[m][n] += s[n] * (C[m][n] - (128 + zp[n]) * S_m)
 // (the reference's identity, src/kernels/gemv_w4a16.cuh:25-37, with the group
-// sum computed by the matrix core instead of a prologue kernel). The W waves of
-// a workgroup take interleaved blocks of each tile (two loads in flight, then
-// two blocks of math; latency is hidden by occupancy) and are summed in LDS.
+// sum computed by the matrix core instead of a prologue kernel).
 //
-// Split tiles, without fences or L2 flushes (each XCD has its own L2; a
-// device-scope fence per workgroup costs more than the weight stream):
+// k_rows (default). Data-parallel: a workgroup owns whole units (S row quads
+// of a tile over all of K), its W waves split K and are summed in LDS in wave
+// order; no workgroup exchanges partials with another, so a launch ends when
+// its loads end. Items (one group of one unit) are loaded D ahead, either
+// into registers or -- the default -- straight into per-wave LDS slots
+// (buffer_load ... lds), which bounds the depth by LDS instead of registers.
+// M = 1 stages x in LDS once per workgroup. Epilogues: bf16 / fp32 output,
+// residual add, swiglu of gate|up pairs, rmsnorm of x in LDS before the
+// projection, and the fused argmax.
+//
+// k_skinny (QW4_ROWS = 0). Stream-K: a fixed number of workgroups P sized to
+// the chip cuts the flattened list of U = tiles x groups blocks into P equal
+// contiguous ranges; a tile cut by a range boundary ("split tile") is
+// finished by whichever contributor completes it last:
 //  * M = 1: each contributor adds its partial, as 2^-20 fixed point biased by
 //    2^49, into one 64-bit word per output element with a returning
 //    device-scope atomic, together with 1 << 56 as an arrival count. Integer
 //    addition is order-independent (bitwise deterministic), and the contributor
 //    whose add completes the count holds the exact total in the returned value,
-//    rounds it once and emits it, then clears the word. One round trip; a
-//    workgroup's first split tile is stashed in LDS and issued together with its
-//    last at the end, so no wave stalls mid-stream. Limits: |partial| < 2^29
-//    and at most 64 contributors per tile (ranges are kept >= G/60 blocks).
+//    rounds it once and emits it, then clears the word. Limits: |partial| <
+//    2^29 and at most 64 contributors per tile (ranges are kept >= G/60 blocks).
 //  * M > 1: each contributor writes its partial through (16-byte sc1 buffer
 //    stores) to its slot, waits for completion once at the end of the
 //    workgroup, then bumps the tile's counter (one per 128-byte line); the last
 //    one reads all slots back (sc1 loads) in workgroup order and emits.
 // Counters and words reset themselves, so the next call -- or a graph replay --
-// starts from zero. Whole tiles are summed in a fixed order (waves 0..W-1), so
-// every output is bitwise reproducible (the property of gemv_w4a16.cu:262-279).
+// starts from zero. Both kernels sum in a fixed order, so every output is
+// bitwise reproducible (the property of gemv_w4a16.cu:262-279).
 //
 // Output layout per lane: acc[st][jj] is row m = 4q + jj, column
 // n = 64*tile + 4c + st.
