@@ -316,17 +316,25 @@ __device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
   return (int)(((long long)(u + 1) * a.P - 1) / a.U);
 }
 
-// One workgroup per tile (8 waves, the main kernel's wave -> row mapping);
-// tiles that a single workgroup covered were stored by the main kernel.
+// The cut tiles' fp32 partials are summed by many small blocks: block
+// (tile ts, main-kernel wave w, part) owns the m-blocks [part * 4, part * 4 + 4)
+// of wave w's region (the slot layout [wave][m-block][lane] keeps them
+// contiguous), so a cut tile is read by 16 blocks at once instead of one
+// workgroup. Tiles a single workgroup covered were stored by the main kernel.
+constexpr int kFixParts = 2;   // parts per main-kernel wave region
+
 template <int NH>
-__global__ __launch_bounds__(512) void k_gemm_fixup(GemmArgs a) {
+__global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
   constexpr int MBW = G2_MB / NH;
-  const int ts = blockIdx.x;   // split tile full + ts
+  constexpr int kPer = G2_MB / kFixParts;   // (half, m-block) pairs per block
+  const int ts = blockIdx.x / (G2_WAVES * kFixParts);   // split tile full + ts
+  const int wave = (blockIdx.x / kFixParts) % G2_WAVES;
+  const int part = blockIdx.x % kFixParts;
   const int t = a.full + ts;
   const int p0 = g2_owner_of(a, ts * a.G), p1 = g2_owner_of(a, ts * a.G + a.G - 1);
   if (p0 == p1) return;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
+  const int r = lane & 31, h = lane >> 5;
   const int wt = NH == 1 ? (wave >> 1) : (wave & 3);
   const int b0 = NH == 1 ? (wave & 1) : 0;
   const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;
@@ -336,27 +344,37 @@ __global__ __launch_bounds__(512) void k_gemm_fixup(GemmArgs a) {
   if (tile * kTileN >= a.N) return;
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)(2u * a.P * kSlotBytes), 0x00020000);
-  f32x16v acc[NH][MBW];
+  f32x16v acc[kPer];
 #pragma unroll
-  for (int j = 0; j < NH; ++j)
-#pragma unroll
-    for (int mb = 0; mb < MBW; ++mb) acc[j][mb] = f32x16v{};
+  for (int e = 0; e < kPer; ++e) acc[e] = f32x16v{};
   for (int pp = p0; pp <= p1; ++pp) {
     const int which = (g2_range_start(a, pp) / a.G == ts) ? 0 : 1;
 #pragma unroll
-    for (int j = 0; j < NH; ++j)
+    for (int e = 0; e < kPer; ++e) {
+      const uint32_t off = g2_slot_off(pp, which, wave, part * kPer + e, lane);
 #pragma unroll
-      for (int mb = 0; mb < MBW; ++mb) {
-        const uint32_t off = g2_slot_off(pp, which, wave, j * MBW + mb, lane);
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc[j][mb][4 * i + e] += __uint_as_float(v[e]);
-        }
+        for (int c = 0; c < 4; ++c) acc[e][4 * i + c] += __uint_as_float(v[c]);
       }
+    }
   }
-  g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+  // pair index j * MBW + mb (g2_slot_store's order)
+  const int m0 = tm * G2_BM;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int idx = part * kPer + e, j = idx / MBW, mb = idx % MBW;
+    const int m = m0 + 32 * (mw + mb) + r;
+    if (m >= a.M) continue;
+    uint16_t* crow = a.C + (size_t)m * a.N + tile * kTileN;
+#pragma unroll
+    for (int jq = 0; jq < 4; ++jq) {
+      const u32x2 o = {pack_bf16x2(acc[e][4 * jq], acc[e][4 * jq + 1]),
+                       pack_bf16x2(acc[e][4 * jq + 2], acc[e][4 * jq + 3])};
+      *reinterpret_cast<u32x2*>(crow + 4 * (8 * (b0 + j) + 2 * jq + h)) = o;
+    }
+  }
 }
 
 template <int NH>
@@ -485,8 +503,8 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     //  * per tile: one workgroup per tile, ceil(nt / CUs) G;
     //  * stream-K: one workgroup per CU, all nt G (tile, group) units split
     //    evenly, nt G / CUs + 16 (two fp32 partial tiles written per
-    //    workgroup) + 0.75 per piece of a cut tile (k_gemm_fixup reads the
-    //    pieces of a tile one after another);
+    //    workgroup) + 0.1 per piece of a cut tile (k_gemm_fixup's blocks read
+    //    a tile's pieces one after another);
     //  * hybrid: whole tiles for the floor(nt / CUs) full rounds, then the
     //    other nt % CUs tiles split over the CUs: the same work, one partial
     //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile.
@@ -499,8 +517,8 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     const int rem = nt % cus;
     const double t_dp = (double)((nt + cus - 1) / cus) * G;
     const double work = (double)nt * G / cus;
-    const double t_sk = work + 16.0 + 0.75 * ((cus + nt - 1) / nt + 1);
-    const double t_hy = work + 8.0 + 0.75 * (rem ? (cus + rem - 1) / rem + 1 : 0);
+    const double t_sk = work + 16.0 + 0.1 * ((cus + nt - 1) / nt + 1);
+    const double t_hy = work + 8.0 + 0.1 * (rem ? (cus + rem - 1) / rem + 1 : 0);
     const bool ws_ok = ws && ws->buf && ws->bytes >= gemm_workspace_need(cus) && cus % 8 == 0 &&
                        rem != 0 && (long long)nt * G < (1LL << 31);
     const bool sk_ok = ws_ok && (long long)nt * G >= 2LL * cus;
@@ -530,8 +548,9 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     else k_gemm<1><<<grid, 512, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
     if (a.full != nt) {   // the split tiles
-      if (nh == 2) k_gemm_fixup<2><<<nt - a.full, 512, 0, s>>>(a);
-      else k_gemm_fixup<1><<<nt - a.full, 512, 0, s>>>(a);
+      const int fb = (nt - a.full) * G2_WAVES * kFixParts;
+      if (nh == 2) k_gemm_fixup<2><<<fb, 64, 0, s>>>(a);
+      else k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;
