@@ -463,7 +463,7 @@ class Bench:
             "bound": "mfma", "achieved": round(pf_tf, 1), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(pf_tf / BF16_PEAK_TFLOPS, 4),
             "traffic": traffic_from_profiles("k_gemm"),
-            "kernel": "k_gemm (+ k_gemm_fixup when stream-K), M=4096, gate 17408x5120 + "
+            "kernel": "k_gemm (+ k_gemm_fixup when tiles are split), M=4096, gate 17408x5120 + "
                       "down 5120x17408"}
         log(f"config4: {c4}")
         return pf_tf
