@@ -1,7 +1,7 @@
 """Benchmark of the MI355X W4A16 hot path. Prints ONE JSON line.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers 64] [--no-cpu]
-                    [--only-decode | --only-prefill]
+                    [--only-decode | --only-verify | --only-prefill]
 
 Headline: the decode GEMV sweep of a full layer --
 qkv (5120->7168), o (4096->5120), gate|up (5120->34816), down (17408->5120) --
@@ -10,7 +10,7 @@ far beyond the 256 MB MALL). One step = one decoded token's body: all 256 GEMV
 launches (M=1). value = algorithmic bytes / time (GB/s), inputs resident in HBM.
 
 Also reported (in "extra"): config 1 (single 5120x5120 GEMV), config 3 (verify
-M=9/12/16 over the same 64-layer sweep), config 4 (prefill GEMM TFLOPS at
+M=9/12/16 over the same 64-layer sweep, and per projection at M=9/16), config 4 (prefill GEMM TFLOPS at
 M=512/1024/4096), config 5 (lm_head 248320x5120 + fused argmax, M=1/9), the
 measured streaming-read HBM bandwidth, and the CPU baseline (the oracle's port
 of the reference's host dequant+matmul) on a bounded sample.
@@ -19,8 +19,9 @@ Algorithmic bytes (4-bit zeros): K*N/2 + (K/128)*N*2 + (K/128)*N/2 + M*K*2 + M*N
 
 roofline.traffic (HBM bytes per launch of the decode kernel) is read from
 profiles/traffic.json, the FETCH_SIZE + WRITE_SIZE summary of the rocprofv3
-counter runs of this same command (null if absent). --only-decode and
---only-prefill run one part (for profiling); the default runs everything.
+counter runs of this same command (null if absent). --only-decode,
+--only-verify (the decode sweep, then config 3) and --only-prefill run one part
+(for profiling); the default runs everything.
 """
 from __future__ import annotations
 
@@ -246,6 +247,37 @@ class Bench:
         return {"value": value, "ms": ms, "step_bytes": step_bytes, "avg_bytes": avg_bytes,
                 "avg_ms": avg_ms}
 
+    # ---------------------------------------------------------- config 3
+    def verify(self):
+        """Speculative-verify sweeps (M = 9, 12, 16) over the decode layers, and
+        per projection (graphs of the layers' launches of one projection)."""
+        hip, torch = self.hip, self.torch
+        xs, ys, scratch = self.xs, self.ys, self.scratch
+        g_m1 = self.capture(lambda: self.step(1))
+        t1 = self.time_graph(g_m1, 5)
+        del g_m1
+        c3 = {}
+        for M in (9, 12, 16):
+            g = self.capture(lambda: self.step(M))
+            t = self.time_graph(g, 5)
+            del g
+            byts = sum(alg_bytes(M, K, N) for _, K, N in LAYER) * len(self.layers)
+            c3[f"M{M}"] = {"ms_per_sweep": round(t, 3), "GBps": round(byts / (t * 1e-3) / 1e9, 1),
+                           "x_of_M1": round(t / t1, 3)}
+        per = {}
+        for M in (9, 16):
+            for li, (name, K, N) in enumerate(LAYER):
+                g1 = self.capture(lambda: [hip.gemm_small_w4a16(ys, lw[li], xs[K], M, scratch)
+                                           for lw in self.layers])
+                d = self.time_graph(g1, 3) / len(self.layers)
+                del g1
+                b = alg_bytes(M, K, N)
+                per[f"M{M} {name}"] = {"us": round(d * 1e3, 2),
+                                       "GBps": round(b / (d * 1e-3) / 1e9, 1)}
+        c3["per_projection"] = per
+        self.extra["config3_verify"] = c3
+        log(f"config3: {c3}")
+
     # ------------------------------------------------------- configs 1, 3, 5
     def others(self):
         hip, torch = self.hip, self.torch
@@ -261,20 +293,7 @@ class Bench:
                                  "note": "13.6 MB, 100 calls in one graph: MALL-resident"}
         log(f"config1: {us:.2f} us")
 
-        step_bytes1 = sum(alg_bytes(1, K, N) for _, K, N in LAYER) * len(self.layers)
-        g_m1 = self.capture(lambda: self.step(1))
-        t1 = self.time_graph(g_m1, 5)
-        del g_m1
-        c3 = {}
-        for M in (9, 12, 16):
-            g = self.capture(lambda: self.step(M))
-            t = self.time_graph(g, 5)
-            del g
-            byts = sum(alg_bytes(M, K, N) for _, K, N in LAYER) * len(self.layers)
-            c3[f"M{M}"] = {"ms_per_sweep": round(t, 3), "GBps": round(byts / (t * 1e-3) / 1e9, 1),
-                           "x_of_M1": round(t / t1, 3)}
-        self.extra["config3_verify"] = c3
-        log(f"config3: {c3}")
+        self.verify()
 
         # One GPU's share of an 8-way tensor-parallel layer (qkv and gate|up split
         # by rows, o and down by columns; the all-reduce after o/down is not
@@ -478,6 +497,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only-decode", action="store_true")
     ap.add_argument("--only-prefill", action="store_true")
+    ap.add_argument("--only-verify", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the W4A16 path is single-GPU; "
@@ -492,6 +512,11 @@ def main():
                           "unit": "TFLOP/s", "n_gpus": 1, "extra": bench.extra}), flush=True)
         return
     d = bench.decode()
+    if args.only_verify:
+        bench.verify()
+        print(json.dumps({"metric": "verify sweep GB/s", "n_gpus": 1, "extra": bench.extra}),
+              flush=True)
+        return
     if not args.only_decode:
         bench.others()
         bench.prefill()
