@@ -1396,12 +1396,16 @@ void launch_rows_x(const SkinnyArgs& a, int S, hipStream_t st) {
 }
 
 // Dynamic LDS above the default limit is allowed once per kernel.
-template <class K>
-void allow_lds(K kern, int bytes) {
+// Dynamic LDS above the default limit is allowed per kernel (one cache per
+// kernel instantiation), once per device. qw4_scratch_alloc raises every
+// LDS-DMA kernel to its maximum, so no launch -- captured into a graph or not
+// -- has to.
+template <auto Kern>
+void allow_lds(int bytes) {
   static int set[64] = {0};
   int& v = set[current_device()];
   if (bytes > v) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess)
       v = bytes;
   }
@@ -1410,9 +1414,50 @@ void allow_lds(K kern, int bytes) {
 template <int OUT, int FMT, int S, int W, int D, bool XL>
 void launch_rows_dma_d(const SkinnyArgs& a, hipStream_t st) {
   const int lds = (XL ? a.M * a.K * 2 : 0) + W * D * DmaSlot<FMT, S>::kUnits * 16;
-  auto kern = k_rows<OUT, FMT, S, W, XL, D, true>;
-  allow_lds(kern, lds);
+  constexpr auto kern = &k_rows<OUT, FMT, S, W, XL, D, true>;
+  allow_lds<kern>(lds);
   kern<<<a.P, 64 * W, lds, st>>>(a);
+}
+
+template <int OUT, int FMT, int S, bool XL, int D>
+void prepare_dma_one() {
+  constexpr auto kern = &k_rows<OUT, FMT, S, 8, XL, D, true>;
+  hipFuncAttributes at{};
+  if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kern)) == hipSuccess)
+    allow_lds<kern>(kLdsBytes - (int)at.sharedSizeBytes);
+}
+
+// Every LDS-DMA kernel the launch code can pick (launch_rows_dma).
+template <int OUT, int FMT>
+void prepare_dma_out() {
+  prepare_dma_one<OUT, FMT, 2, true, 2>();
+  prepare_dma_one<OUT, FMT, 2, true, 3>();
+  prepare_dma_one<OUT, FMT, 2, true, 4>();
+  if constexpr (OUT != OUT_NORM) {
+    prepare_dma_one<OUT, FMT, 2, false, 2>();
+    prepare_dma_one<OUT, FMT, 2, false, 3>();
+    prepare_dma_one<OUT, FMT, 2, false, 4>();
+    prepare_dma_one<OUT, FMT, 4, false, 2>();
+    if constexpr (OUT != OUT_ARGMAX) {
+      prepare_dma_one<OUT, FMT, 4, false, 3>();
+      prepare_dma_one<OUT, FMT, 4, false, 4>();
+    }
+  }
+}
+
+void prepare_dma_lds() {
+  static bool done[64] = {false};
+  bool& d = done[current_device()];
+  if (d) return;
+  prepare_dma_out<OUT_BF16, 4>();
+  prepare_dma_out<OUT_F32, 4>();
+  prepare_dma_out<OUT_ARGMAX, 4>();
+  prepare_dma_out<OUT_RES, 4>();
+  prepare_dma_out<OUT_SWIGLU, 4>();
+  prepare_dma_out<OUT_NORM, 4>();
+  prepare_dma_out<OUT_BF16, 8>();
+  prepare_dma_out<OUT_ARGMAX, 8>();
+  d = true;
 }
 
 // LDS-DMA items: units of S row quads, 8 waves, D items per wave; staged
@@ -1620,6 +1665,7 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
     qw4_scratch_free(s);
     return QW4_ERR_NOMEM;
   }
+  prepare_dma_lds();
   return QW4_OK;
 }
 
