@@ -1332,8 +1332,9 @@ Launch launch_for(int out_f, int G, int M) {
   // M = 1: LDS-DMA items with 32-row units and 8 waves, when the slots fit
   // the CU's LDS next to the staged activations. Measured on MI355X over the
   // model's projections and heads: 4 items per wave when the output has at
-  // least as many 64-row tiles as CUs, 3 for long K (>= 64 groups), else 2
-  // (deeper is slower); the 4-bit GEMV and its residual / swiglu / argmax
+  // least 1.5 64-row tiles per CU (3+ units per workgroup; at 1 tile per CU,
+  // a 16384-row projection, 2 is 6% faster), 3 for long K (>= 64 groups),
+  // else 2 (deeper is slower); the 4-bit GEMV and its residual / swiglu / argmax
   // epilogues gain up to 8%, while the fused rmsnorm and the 8-bit head run
   // faster with register items, which stay their default. QW4_DMA = 0 keeps
   // register items, 2 | 3 | 4 forces LDS-DMA items of that depth for every
@@ -1344,7 +1345,7 @@ Launch launch_for(int out_f, int G, int M) {
     const char* ed = std::getenv("QW4_DMA");
     const int dd = ed ? std::atoi(ed)
                    : (OUT == OUT_NORM || FMT == 8) ? 0
-                                                   : (tiles >= device_cus() ? 4 : (G >= 64 ? 3 : 2));
+                   : (2 * tiles >= 3 * device_cus() ? 4 : (G >= 64 ? 3 : 2));
     const int slot = (FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256);
     const int need = xbytes + 8 * dd * slot + 2 * 8 * 2 * 16 * 16 + (OUT == OUT_NORM ? 64 : 0);
     if (dd >= 2 && dd <= 4 && xbytes <= rows_xchunks(true) * 16 * 64 * 8 && need <= kLdsBytes) {
