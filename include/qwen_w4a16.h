@@ -212,7 +212,7 @@ int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
  * x through the GEMV (T = 1), the skinny kernel in chunks of up to 16 rows
  * (2 <= T <= max_t), or the prefill GEMM (T > max_t). max_t is the crossover
  * measured on MI355X for this weight's size (qw4_linear_max_t: 48 rows for
- * a 93 MB projection, 176 for an 11 MB one); env QW4_LIN_MAX_T overrides it,
+ * a 93 MB projection, 112 for an 11 MB one); env QW4_LIN_MAX_T overrides it,
  * as QWEN_MMA_MAX_T does in the reference. ws may be NULL. */
 int qw4_linear(uint16_t* y, const qw4_weights* w, const uint16_t* x, int T, qw4_scratch* s,
                qw4_workspace* ws, void* stream);

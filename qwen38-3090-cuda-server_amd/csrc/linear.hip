@@ -9,16 +9,17 @@
 namespace {
 
 // Rows up to which 16-row skinny passes beat the prefill GEMM. Measured on
-// MI355X over the model's projections: a skinny pass costs about
-// 0.37 us per MB of weights + 10 us, the prefill GEMM 100-150 us at these row
-// counts, so the crossover is near 16 * 370 / (MB + 20) rows -- 48 for gate|up
-// (93 MB), 80 for down (46 MB), 144 for qkv (19 MB), 176 for o_proj (11 MB).
+// MI355X over the model's projections (T = 16 .. 256): a skinny pass costs
+// about 0.245 us per MB of weights + 5.8 us, the prefill GEMM about 60 us +
+// 0.4 us per MB at these row counts, so the crossover is 16 whole passes
+// under their ratio -- 48 rows for gate|up (93 MB; measured ~55), 64 for down
+// (46 MB; ~60), 96 for qkv (19 MB; ~107), 112 for o_proj (11 MB; ~127).
 int lin_max_t(const qw4_weights* w) {
   const char* e = std::getenv("QW4_LIN_MAX_T");
   const int v = e ? std::atoi(e) : 0;
   if (v > 0) return v;
   const double mb = (double)w->out_f * w->in_f * (0.5 + 2.5 / 128) / 1e6;
-  const int chunks = (int)(370.0 / (mb + 20.0));
+  const int chunks = (int)((60.0 + 0.4 * mb) / (0.245 * mb + 5.8));
   return 16 * (chunks < 1 ? 1 : chunks);
 }
 

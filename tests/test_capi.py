@@ -122,9 +122,9 @@ def test_cpp_layer_exports_every_declared_function(hip):
 
 def test_linear_threshold_by_weight_size(hip, monkeypatch):
     """linear()'s skinny/prefill crossover per weight (host-only call): the
-    model's projections get 48 (gate|up), 80 (down), 144 (qkv), 176 (o_proj)."""
+    model's projections get 48 (gate|up), 64 (down), 96 (qkv), 112 (o_proj)."""
     monkeypatch.delenv("QW4_LIN_MAX_T", raising=False)
-    want = {(34816, 5120): 48, (5120, 17408): 80, (7168, 5120): 144, (5120, 4096): 176}
+    want = {(34816, 5120): 48, (5120, 17408): 64, (7168, 5120): 96, (5120, 4096): 112}
     for (n, k), t in want.items():
         w = hip.W4A16Weights()
         w.out_f, w.in_f, w.group_size, w.num_groups = n, k, 128, k // 128

@@ -211,7 +211,7 @@ def workspace(hip):
 def test_linear_paths(hip, orc, scratch, workspace):
     """linear() picks the GEMV (T = 1), 16-row skinny chunks (T <= max_t) or the
     prefill GEMM, and matches each path run directly."""
-    N, K = 1024, 2048   # 1.1 MB: skinny passes up to 16 * 17 rows
+    N, K = 1024, 2048   # 1.1 MB: skinny passes up to 16 * 9 rows
     q, zp, s = orc.gen_weights(N, K, seed=8, tensor=5)
     w = repack_from_logical(hip, orc, q, zp, s)
     mt = hip.linear_max_t(w)
