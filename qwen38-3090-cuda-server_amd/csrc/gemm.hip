@@ -97,7 +97,7 @@ __device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const G2Rsr
     for (int s = 0; s < 2; ++s)
       wg.q[j][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.qw, ((2 * s + h) * 64 + p) * 16,
                                                          blk * 4096u, 0);
-    wg.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (4 * a16 + (r & 3)) * 2, blk * 128u, 0);
+    wg.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (4 * a16 + (r & 3)) * 2, blk * (uint32_t)kMetaBytes, 0);
     wg.z[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.zr, a16 * 2, blk * 32u, 0);
   }
 }
@@ -401,8 +401,9 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
   G2Rsrc wr;
   wr.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0,
                                             (int)((uint32_t)a.N * (uint32_t)a.K / 2u), 0x00020000);
-  wr.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0,
-                                            (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
+  wr.sc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.sc), 0,
+      (int)((uint32_t)a.N / kTileN * (uint32_t)a.G * (uint32_t)kMetaBytes), 0x00020000);
   wr.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
                                             (int)((uint32_t)a.N * (uint32_t)a.G / 2u), 0x00020000);
   for (int t = vp; t < a.full; t += a.P) {

@@ -80,10 +80,11 @@ __global__ void k_repack_meta(uint16_t* __restrict__ dscale, uint16_t* __restric
       s = sscale[(size_t)g * n_src + ns];
       zn = (szero[(size_t)g * (n_src / 8) + (ns >> 3)] >> (4 * awq_slot(ns & 7))) & 0xFu;
     }
-    dscale[blk * 64 + 4 * c + i] = s;
+    dscale[blk * kMetaU16 + 4 * c + i] = s;
     z |= zn << (4 * i);
   }
   dzero[blk * 16 + c] = (uint16_t)z;
+  dscale[blk * kMetaU16 + 64 + c] = (uint16_t)z;
 }
 
 // ----------------------------------------------------------------- dequant
@@ -100,7 +101,7 @@ __global__ void k_dequant_rows(uint16_t* __restrict__ dst, const uint32_t* __res
   const int g = wi >> 4, j = (wi >> 2) & 3, w = wi & 3;
   const size_t blk = (size_t)b * G + g;
   const uint32_t word = qw[blk * kWordsPerBlock + j * 256 + tile_pos_of_row(rr) * 4 + w];
-  const float s = bf16_bits_to_f32(sc[blk * 64 + rr]);
+  const float s = bf16_bits_to_f32(sc[blk * kMetaU16 + rr]);
   const int z = (zr[blk * 16 + (rr >> 2)] >> (4 * (rr & 3))) & 0xF;
   uint32_t o[4];
 #pragma unroll
@@ -339,7 +340,7 @@ int qw4_version(void) { return 1; }
 size_t qw4_weights_bytes(const qw4_weights* w) {
   if (!w) return 0;
   const size_t n = (size_t)w->out_f, k = (size_t)w->in_f, g = (size_t)w->num_groups;
-  return n * k / 2 + n * g * 2 + n * g / 2;
+  return n * k / 2 + n * g * kMetaBytes / kTileN + n * g / 2;
 }
 
 int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void* stream) {
@@ -354,7 +355,7 @@ int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void*
   w->num_groups = in_f / group_size;
   const size_t n = (size_t)out_f, g = (size_t)w->num_groups;
   hipError_t e = hipMalloc((void**)&w->qweight, n * in_f / 2);
-  if (e == hipSuccess) e = hipMalloc((void**)&w->scale, n * g * 2);
+  if (e == hipSuccess) e = hipMalloc((void**)&w->scale, n * g * kMetaBytes / kTileN);
   if (e == hipSuccess) e = hipMalloc((void**)&w->zeros, n * g / 2);
   if (e != hipSuccess) {
     set_hip_error((int)e);

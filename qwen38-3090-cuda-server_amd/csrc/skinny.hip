@@ -49,6 +49,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -167,8 +168,11 @@ __device__ __forceinline__ SkinnyRsrc skinny_rsrc(const SkinnyArgs& a) {
   SkinnyRsrc r;
   r.qw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0, (int)a.weight_bytes,
                                            0x00020000);
-  r.sc = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0,
-                                           (int)((uint32_t)a.N * (uint32_t)a.G * 2u), 0x00020000);
+  // 4-bit: 160-byte (scale, zero-point) records per block; 8-bit: 128 bytes of scales
+  r.sc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.sc), 0,
+      (int)((uint32_t)a.N / kTileN * (uint32_t)a.G * (a.zr ? (uint32_t)kMetaBytes : 128u)),
+      0x00020000);
   r.zr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0,
                                            a.zr ? (int)((uint32_t)a.N * (uint32_t)a.G / 2u) : 0,
                                            0x00020000);
@@ -188,7 +192,7 @@ __device__ __forceinline__ void load_group(GroupData& d, const SkinnyRsrc& r, co
 #pragma unroll
   for (int t = 0; t < 4; ++t)
     d.x[t] = __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
-  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * 128u, 0);
+  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * (uint32_t)kMetaBytes, 0);
   d.z = __builtin_amdgcn_raw_buffer_load_b16(r.zr, (uint32_t)c * 2u, blk * 32u, 0);
 }
 
@@ -630,6 +634,7 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
                                           uint32_t xoff) {
   constexpr uint32_t kBlk = FMT == 8 ? 8192u : 4096u;
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;   // bytes of one row quad in a chunk
+  constexpr uint32_t kScB = FMT == 8 ? 128u : (uint32_t)kMetaBytes;   // scale bytes per block
 #pragma unroll
   for (int i = 0; i < S; ++i)
 #pragma unroll
@@ -643,14 +648,14 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
           __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
   }
   if (S == 4) {
-    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r.sc, soff, blk * 128u, 0);
+    const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r.sc, soff, blk * kScB, 0);
     d.s[0] = v[0];
     d.s[(S + 1) / 2 - 1] = v[1];
   } else if (S == 2) {
-    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff, blk * 128u, 0);
+    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff, blk * kScB, 0);
   } else {
     // the aligned word holding this row's scale (half st0 & 1)
-    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff & ~3u, blk * 128u, 0);
+    d.s[0] = __builtin_amdgcn_raw_buffer_load_b32(r.sc, soff & ~3u, blk * kScB, 0);
   }
   // 32-bit loads only: a 16-bit load result gets masked right after the load,
   // which makes the compiler wait for it there (zoff: the aligned word holding
@@ -724,7 +729,8 @@ __device__ __forceinline__ void dma_issue(u32x4* slot, const SkinnyRsrc& r, uint
 #pragma unroll
     for (int h = 0; h < L::kH; ++h)
       dma_load16(r.qw, slot + (i * L::kH + h) * 64, woff + i * kQuad + h * 16, blk * kBlk);
-  dma_load4(r.sc, slot + L::kNQ * 64, (uint32_t)(lane & 31) * 4u, blk * 128u);
+  dma_load4(r.sc, slot + L::kNQ * 64, (uint32_t)(lane & 31) * 4u,
+            blk * (FMT == 8 ? 128u : (uint32_t)kMetaBytes));
   if (FMT == 4) dma_load4(r.zr, slot + L::kNQ * 64 + 16, (uint32_t)(lane & 7) * 4u, blk * 32u);
 }
 
@@ -1125,6 +1131,385 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   if constexpr (DMA) wait_vm<0>();
 }
 
+// ------------------------------------------------- decode with integer MFMA
+// k_dec: M = 1, 4-bit weights. The work split and epilogues are k_rows's
+// (whole units per workgroup, waves split K, unit sums in LDS in wave order);
+// items are loaded into registers, D per wave (or into LDS slots, DMA); the
+// math per item is integer:
+//  * activations: each 128-group of x (bf16) is written as the integers
+//    X = rne(x * 2^e_g), e_g chosen so that max |X| lies in [2^20, 2^21) --
+//    exact for every element within 13 binades of the group's largest, and
+//    within 2^-22 of it for the rest -- and split into bytes,
+//    X = 65536 a + 256 b + c with a in [-32, 32], b, c in [-128, 127]: rows 0,
+//    1, 2 of the int8 A operand of v_mfma_i32_16x16x64_i8 (rows 3..15 repeat
+//    row 2; their outputs are not used). Per group the LDS also holds 2^-e_g,
+//    -sum(256 a + b) and -sum c.
+//  * weights: the low nibbles of a lane's four packed words (w & 0x0F0F0F0F)
+//    and the high ones ((w >> 4) & 0x0F0F0F0F) are two int8 B operands of 16 k
+//    each (the activation layout follows the nibble order): 3 VALU per word,
+//    and 2 MFMAs per row quad and group give all three byte rows.
+//  * per row and group, exact in int32 (|V1| <= 15 * 2^13 * 128):
+//    V1 = 256 D[0] + D[1] - zp * sum(256 a + b),  V2 = D[2] - zp * sum c,
+//    acc += (256 V1 + V2) * (s * 2^-e_g) in fp32.
+// The activation rounding is the only departure from the exact dot product
+// (relative 2^-21 per element at most); the rest is fp32 accumulation.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDecPrepIters = 8;   // per-wave prep rounds of 4 groups: G <= 32 W
+constexpr int kDecQ = 24;          // 16-byte operand chunks per group in LDS
+
+// Row-of-16 reductions (DPP): xor 1, xor 2, half-row mirror, row mirror.
+__device__ __forceinline__ uint32_t row16_max(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false));
+  return v;
+}
+__device__ __forceinline__ int row16_sum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);
+  return v;
+}
+__device__ __forceinline__ int sum4_i8(uint32_t w, int acc) {
+  return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
+}
+
+// Activation operands of one group in LDS (384 bytes): parts
+// [L_a | L_b | L_c | H_a | H_b | H_c] x [k chunk q][word r][byte b], where
+// L / H are the k held in the low / high nibbles of a weight byte:
+// k = 128 g + 32 q + 8 r + {0, 4, 1, 5}[b] (L) or {2, 6, 3, 7}[b] (H).
+// The lane that prepares chunk c16 = 4 q + r of group g (8 bf16 in v) writes
+// word c16 of each part and, for c16 = 0, the group's constants.
+__device__ __forceinline__ void dec_prep_chunk(uint32_t* xw, u32x4* cst, int g, int c16,
+                                               const u32x4& v, bool valid) {
+  float f[8];
+  uint32_t m = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = __uint_as_float(v[e] << 16);
+    f[2 * e + 1] = __uint_as_float(v[e] & 0xffff0000u);
+    m = max(m, max(v[e] << 17 >> 1, v[e] & 0x7fff0000u));
+  }
+  m = row16_max(m);   // |x| bits of the group's largest element
+  // 2^sh scales it into [2^20, 2^21): 1.5 * 2^23 + 0x8080 + X stays in
+  // [2^23, 2^24), where the fp32 ulp is 1
+  const int sh = min(20 - ((int)(m >> 23) - 127), 126);
+  const float p2 = __uint_as_float((uint32_t)(sh + 127) << 23);
+  const float inv = __uint_as_float((uint32_t)(127 - sh) << 23);
+  // T = X + 0x8080: byte 0 = c + 128, byte 1 = b + 128, byte 2 = a
+  uint32_t t[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    t[j] = __float_as_uint(__builtin_fmaf(f[j], p2, 12615808.0f)) - 0x4B400000u;
+  uint32_t o[6];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {   // L: elements 0, 4, 1, 5; H: 2, 6, 3, 7
+    const uint32_t e0 = t[2 * h], e4 = t[2 * h + 4], e1 = t[2 * h + 1], e5 = t[2 * h + 5];
+    const uint32_t pa = __builtin_amdgcn_perm(e4, e0, 0x05010400u);   // e0.b0 e4.b0 e0.b1 e4.b1
+    const uint32_t pb = __builtin_amdgcn_perm(e5, e1, 0x05010400u);
+    const uint32_t pc = __builtin_amdgcn_perm(e4, e0, 0x0C0C0602u);   // e0.b2 e4.b2
+    const uint32_t pd = __builtin_amdgcn_perm(e5, e1, 0x0C0C0602u);
+    o[3 * h] = __builtin_amdgcn_perm(pd, pc, 0x05040100u);
+    o[3 * h + 1] = __builtin_amdgcn_perm(pb, pa, 0x07060302u) ^ 0x80808080u;
+    o[3 * h + 2] = __builtin_amdgcn_perm(pb, pa, 0x05040100u) ^ 0x80808080u;
+  }
+  int sy = (sum4_i8(o[0], sum4_i8(o[3], 0)) << 8) + sum4_i8(o[1], sum4_i8(o[4], 0));
+  int sc = sum4_i8(o[2], sum4_i8(o[5], 0));
+  sy = row16_sum(sy);
+  sc = row16_sum(sc);
+  if (valid) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) xw[g * (kDecQ * 4) + k * 16 + c16] = o[k];
+    if (c16 == 0)
+      cst[g] = u32x4{__float_as_uint(inv), (uint32_t)(-sy), (uint32_t)(-sc), 0u};
+  }
+}
+
+template <int S>
+__device__ __forceinline__ void dec_mma(float (&acc)[S], const RowsData<4, S, true>& d,
+                                        const u32x4* xg, u32x4 cs, int aoff, int st0, int zsh) {
+  const i32x4 AL = __builtin_bit_cast(i32x4, xg[aoff]);
+  const i32x4 AH = __builtin_bit_cast(i32x4, xg[12 + aoff]);
+  const float inv = __uint_as_float(cs[0]);
+  const int ny = (int)cs[1], nc = (int)cs[2];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    i32x4 BL, BH;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      BL[r] = (int)(d.w[i][0][r] & 0x0F0F0F0Fu);
+      BH[r] = (int)((d.w[i][0][r] >> 4) & 0x0F0F0F0Fu);
+    }
+    i32x4 Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(AL, BL, i32x4{0, 0, 0, 0}, 0, 0, 0);
+    Dm = __builtin_amdgcn_mfma_i32_16x16x64_i8(AH, BH, Dm, 0, 0, 0);
+    const int zp = (int)((d.z >> (zsh + 4 * (st0 + i))) & 0xFu);
+    const int v1 = (Dm[0] << 8) + Dm[1] + __mul24(zp, ny);
+    const int v2 = Dm[2] + __mul24(zp, nc);
+    const float val = __builtin_fmaf((float)v1, 256.0f, (float)v2);
+    const uint32_t sbits = (d.s[i >> 1] >> (16 * (S == 1 ? (st0 & 1) : (i & 1)))) & 0xffffu;
+    acc[i] = __builtin_fmaf(val, bf16_bits_to_f32(sbits) * inv, acc[i]);
+  }
+}
+
+// k_dec item slot (16-byte units): S x 64 weight chunks (lane l's 16 bytes
+// of row quad i at 64 i + l), then the block's 160-byte (scale, zero-point)
+// record in a 256-byte area (lane l's 4 bytes at 4 l; lanes >= 40 repeat
+// word 0).
+template <int S>
+constexpr int kDecSlot = S * 64 + 16;
+
+template <int S>
+__device__ __forceinline__ void dec_issue(u32x4* slot, const SkinnyRsrc& r, uint32_t blk,
+                                          uint32_t woff, int lane) {
+#pragma unroll
+  for (int i = 0; i < S; ++i) dma_load16(r.qw, slot + i * 64, woff + i * 256, blk * 4096u);
+  dma_load4(r.sc, slot + S * 64, lane < 40 ? (uint32_t)lane * 4u : 0u, blk * (uint32_t)kMetaBytes);
+}
+
+template <int S>
+__device__ __forceinline__ void dec_read(RowsData<4, S, true>& d, const u32x4* slot, int lane,
+                                         int st0) {
+  const int c = lane & 15;
+#pragma unroll
+  for (int i = 0; i < S; ++i) d.w[i][0] = slot[i * 64 + lane];
+  const uint32_t* sm = reinterpret_cast<const uint32_t*>(slot + S * 64);
+  if (S == 4) {
+    d.s[0] = sm[2 * c];
+    d.s[(S + 1) / 2 - 1] = sm[2 * c + 1];
+  } else {
+    d.s[0] = sm[(4 * c + st0) >> 1];
+  }
+  d.z = sm[32 + (c >> 1)];
+}
+
+// LDS of k_dec (16-byte units): operands 24 G | constants G | OUT_NORM: the
+// staged x (K / 8) | the waves' item slots.
+__host__ __device__ constexpr int dec_lds_units(int K, int G, bool norm, int S, int W, int D) {
+  return kDecQ * G + G + (norm ? K / 8 : 0) + W * D * (S * 64 + 16);
+}
+
+// k_dec: workgroup p owns the whole units [p U / P, (p + 1) U / P) (unit =
+// S row quads of a 64-row tile over all of K; OUT_SWIGLU: (gate, up) unit
+// pairs). Its waves split each unit's groups (wave w takes g = w, w + W, ...,
+// the groups whose activation operands it prepared), keep D items in flight in
+// LDS slots (buffer_load ... lds) across unit boundaries, and at each unit's
+// end sum their partials in LDS in wave order; wave 0 emits. No workgroup
+// exchanges partials with another (measured on MI355X: both a fixed-point
+// atomic exchange of cut units and a flagged pair exchange cost more at the
+// tail than the imbalance of whole units).
+template <int OUT, int S, int W, int D>
+__global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
+  constexpr uint32_t kPer = 4 / S;
+  constexpr uint32_t kQuad = 256u;
+  constexpr int kXC = rows_xchunks(true);
+  __shared__ float red[2][W][S][16];
+  extern __shared__ u32x4 xlds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4, c16 = c;
+  const int aoff = (c < 2 ? c : 2) * 4 + q;
+  const SkinnyRsrc rs = skinny_rsrc(a);
+  const uint32_t zsh = 16 * (c & 1);
+  const uint32_t wbase = Fmt<4>::woff(q, c);
+  const int p = blockIdx.x;
+  const int G = a.G;
+  // OUT_SWIGLU: units 2v (gate v) and 2v + 1 (its up unit), never split
+  const int u0 = OUT == OUT_SWIGLU ? 2 * (int)((long long)p * (a.U / 2) / a.P) : range_start(a, p);
+  const int u1 =
+      OUT == OUT_SWIGLU ? 2 * (int)((long long)(p + 1) * (a.U / 2) / a.P) : range_start(a, p + 1);
+  auto real_unit = [&](int v) {
+    return OUT == OUT_SWIGLU ? ((v & 1) ? (v >> 1) + (int)((uint32_t)a.U / 2u) : (v >> 1)) : v;
+  };
+  Best bs;
+  best_init(bs);
+  const int n16 = a.K / 8;
+  u32x4* const xq = xlds;
+  u32x4* const cst = xlds + kDecQ * G;
+  u32x4* const raw = cst + G;   // OUT_NORM
+  u32x4* const ring = raw + (OUT == OUT_NORM ? n16 : 0) + wave * D * kDecSlot<S>;
+
+  const int nw = wave < G ? (G - 1 - wave) / W + 1 : 0;   // items per unit
+  const int T = nw * (u1 - u0);
+  const uint32_t oob_blk = (uint32_t)a.tiles * (uint32_t)G;
+  int lu = u0, lg = wave;   // load cursor (wave-uniform)
+  auto load_item = [&](int j) __attribute__((always_inline)) {
+    const bool in = lu < u1;
+    const int ru = real_unit(lu);
+    const int st0 = in ? (int)((uint32_t)ru % kPer) * S : 0;
+    const uint32_t blk = in ? (uint32_t)((uint32_t)ru / kPer) * (uint32_t)G + (uint32_t)lg : oob_blk;
+    dec_issue<S>(ring + j * kDecSlot<S>, rs, blk, wbase + (uint32_t)st0 * kQuad, lane);
+    lg += W;
+    if (lg >= G) {
+      lg = wave;
+      ++lu;
+    }
+  };
+  uint32_t* const xw = reinterpret_cast<uint32_t*>(xq);
+  if constexpr (OUT != OUT_NORM) {
+    // x loads of this wave's groups first (g = wave + W (4 it + lane / 16),
+    // chunk lane % 16), then the first weight items; out-of-range chunks
+    // read zeros without traffic
+    u32x4 xv[kDecPrepIters];
+#pragma unroll
+    for (int it = 0; it < kDecPrepIters; ++it) {
+      const int g = wave + W * (4 * it + (lane >> 4));
+      xv[it] = __builtin_amdgcn_raw_buffer_load_b128(
+          rs.x, g < G ? (uint32_t)(g * 16 + c16) * 16u : 0x7ffffff0u, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) load_item(j);
+#pragma unroll
+    for (int it = 0; it < kDecPrepIters; ++it) {
+      if (wave + W * 4 * it >= G) break;   // wave-uniform
+      const int g = wave + W * (4 * it + (lane >> 4));
+      dec_prep_chunk(xw, cst, g, c16, xv[it], g < G);
+    }
+  } else {
+    // rmsnorm of x (src/kernels/elementwise.cu:8-31) in the summation order
+    // of k_rmsnorm (lane l of one wave takes chunks l, l + 64, ..., then a
+    // butterfly), x * rsqrt(mean(x^2) + eps) * (1 + w) rounded to bf16 once;
+    // staged in LDS, then each wave prepares its groups from there
+    u32x4 xv[kXC], nv[kXC];
+    int xi[kXC];
+    const __amdgpu_buffer_rsrc_t rn =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.nw), 0, a.K * 2, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < kXC; ++j) {
+      xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
+      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
+      nv[j] = __builtin_amdgcn_raw_buffer_load_b128(rn, (uint32_t)xi[j] * 16u, 0, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < D; ++j) load_item(j);
+#pragma unroll
+    for (int j = 0; j < kXC; ++j) raw[xi[j]] = xv[j];
+    lds_barrier<true>();
+    __shared__ float rinv;
+    if (wave == 0) {
+      float ss = 0.f;
+      for (int i = lane; i < n16; i += 64) {
+        const u32x4 v = raw[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16_bits_to_f32(v[e] & 0xffffu), hi = bf16_bits_to_f32(v[e] >> 16);
+          ss += lo * lo + hi * hi;
+        }
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
+      if (lane == 0) rinv = rsqrtf(ss / (float)a.K + a.eps);
+    }
+    lds_barrier<true>();
+    const float inv = rinv;
+#pragma unroll
+    for (int j = 0; j < kXC; ++j) {
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t xw2 = xv[j][e], ww = nv[j][e];
+        o[e] = pack_bf16x2(rmsnorm_f32(xw2, ww, inv), rmsnorm_f32(xw2 >> 16, ww >> 16, inv));
+      }
+      raw[xi[j]] = o;
+    }
+    lds_barrier<true>();
+#pragma unroll
+    for (int it = 0; it < kDecPrepIters; ++it) {
+      if (wave + W * 4 * it >= G) break;
+      const int g = wave + W * (4 * it + (lane >> 4));
+      const bool valid = g < G;
+      dec_prep_chunk(xw, cst, g, c16, raw[(valid ? g : 0) * 16 + c16], valid);
+    }
+  }
+
+  float acc[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) acc[i] = 0.f;
+  int par = 0;
+  float gate[OUT == OUT_SWIGLU ? S : 1];   // OUT_SWIGLU: the gate unit's sums (wave 0)
+  // Close unit u: every wave passes here once per unit of the range, in order.
+  auto close_unit = [&](int u) {
+    if (lane < 16) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) red[par][wave][i][lane] = acc[i];
+    }
+    lds_barrier<true>();
+    if (wave == 0) {
+      float t[S];
+#pragma unroll
+      for (int i = 0; i < S; ++i) {
+        float v = red[par][0][i][c];
+        for (int w = 1; w < W; ++w) v += red[par][w][i][c];
+        t[i] = v;
+      }
+      const int ru = real_unit(u);
+      const int b = (int)((uint32_t)ru / kPer), st0 = (int)((uint32_t)ru % kPer) * S;
+      if (OUT == OUT_SWIGLU) {
+        if ((u & 1) == 0) {
+#pragma unroll
+          for (int i = 0; i < S; ++i) gate[i & (OUT == OUT_SWIGLU ? 0xff : 0)] = t[i];
+        } else {
+          f32x4 gg[S], uu[S];
+#pragma unroll
+          for (int i = 0; i < S; ++i) {
+            gg[i] = f32x4{gate[i & (OUT == OUT_SWIGLU ? 0xff : 0)], 0.f, 0.f, 0.f};
+            uu[i] = f32x4{t[i], 0.f, 0.f, 0.f};
+          }
+          emit_swiglu<S>(a, (int)((uint32_t)(u >> 1) / kPer), (int)((uint32_t)(u >> 1) % kPer) * S,
+                         gg, uu, lane);
+        }
+      } else {
+        f32x4 tv[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) tv[i] = f32x4{t[i], 0.f, 0.f, 0.f};
+        emit_rows<OUT, S>(a, b, st0, tv, lane, bs);
+      }
+    }
+    par ^= 1;
+#pragma unroll
+    for (int i = 0; i < S; ++i) acc[i] = 0.f;
+  };
+
+  int cu = u0, cg = wave;   // compute cursor (wave-uniform)
+  int t0 = 0;
+  constexpr int kL = S + 1;   // loads per item
+  // item j waits for its slot (the loads of the D - 1 items after it may
+  // still be in flight)
+  auto step = [&](auto jc, auto nc, bool reload) __attribute__((always_inline)) {
+    constexpr int j = decltype(jc)::value;
+    const int st0 = (int)((uint32_t)real_unit(cu) % kPer) * S;
+    wait_vm<decltype(nc)::value>();
+    RowsData<4, S, true> d;
+    dec_read<S>(d, ring + j * kDecSlot<S>, lane, st0);
+    dec_mma<S>(acc, d, xq + cg * kDecQ, cst[cg], aoff, st0, zsh);
+    if (reload) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      load_item(j);
+    }
+    cg += W;
+    if (cg >= G) {
+      cg = wave;
+      close_unit(cu);
+      ++cu;
+    }
+  };
+  for (; t0 + D <= T; t0 += D)
+    static_for<0, D>([&](auto jc) { step(jc, std::integral_constant<int, (D - 1) * kL>{}, true); });
+  static_for<0, D - 1>([&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (t0 + j < T) step(jc, std::integral_constant<int, (D - 1 - j) * kL>{}, false);
+  });
+  while (cu < u1) {   // waves with no items (wave >= G)
+    close_unit(cu);
+    ++cu;
+  }
+  wait_vm<0>();   // no load lands in LDS after the workgroup released it
+  if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
+}
+
 // ------------------------------------------------------------- host side
 // Workgroups per CU: the kernel's occupancy (all workgroups resident in one
 // round, equal work each). QW4_SKINNY_WGS_PER_CU, QW4_SKINNY_W (4|8|16) and
@@ -1409,7 +1794,105 @@ void allow_lds(int bytes) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
                             hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess)
       v = bytes;
+    else
+      (void)hipGetLastError();   // not sticky: the launch reports what matters
   }
+}
+
+// ---- k_dec launch (M = 1, 4-bit)
+// Tuning override (qw4_tune_decode): all zero = the measured policy below.
+struct DecTune {
+  std::atomic<int> mode{0};   // 0 policy, 1 k_rows for M = 1, 3 k_dec of the given shape
+  std::atomic<int> S{0}, W{0}, D{0}, P{0};
+};
+DecTune g_dec_tune;
+
+struct DecCfg {
+  int S, W, D, P;
+  int lds;   // dynamic LDS bytes
+};
+
+// red + rinv, rounded up (the launch checks the total against the CU's LDS)
+int dec_static_lds(int S, int W) { return 2 * W * S * 16 * 4 + 256; }
+
+// The k_dec instantiations: the first kDecPolicy are the policy's (built for
+// every output mode), the rest tuning alternatives (OUT_BF16 only).
+struct DecVariant {
+  int S, W, D;
+};
+constexpr DecVariant kDecAll[] = {{2, 8, 3}, {2, 8, 2}, {2, 16, 2}, {2, 8, 4},
+                                  {1, 8, 3}, {1, 16, 3}, {2, 4, 4}, {4, 8, 2}};
+constexpr int kDecPolicy = 3;
+constexpr int kDecCount = (int)(sizeof(kDecAll) / sizeof(kDecAll[0]));
+
+// Returns false when the shape does not fit k_dec (activations beyond the
+// per-wave prep, LDS beyond the CU's). Policy, measured on MI355X over the
+// config-2 projections (32-row units throughout; 16-row units and deeper
+// items were slower): 2 items per wave for short K (o_proj, 32 groups), 16
+// waves of 2 items when the output has fewer tiles than CUs and K is long
+// (down: 160 workgroups), else 8 waves of 3 items.
+bool dec_config(int out_f, int G, int OUTmode, DecCfg& c) {
+  const int tiles = out_f / kTileN;
+  const int K = G * kGroup;
+  DecVariant v = (tiles < device_cus() && G >= 64) ? kDecAll[2]
+                 : G <= 32                          ? kDecAll[1]
+                                                    : kDecAll[0];
+  if (OUTmode == OUT_BF16 && g_dec_tune.mode.load(std::memory_order_relaxed) == 3) {
+    const int tS = g_dec_tune.S.load(std::memory_order_relaxed);
+    const int tW = g_dec_tune.W.load(std::memory_order_relaxed);
+    const int tD = g_dec_tune.D.load(std::memory_order_relaxed);
+    bool found = false;
+    for (const DecVariant& x : kDecAll)
+      if ((!tS || x.S == tS) && (!tW || x.W == tW) && (!tD || x.D == tD)) {
+        v = x;
+        found = true;
+        break;
+      }
+    if (!found) return false;
+  }
+  c.S = v.S;
+  c.W = v.W;
+  c.D = v.D;
+  if (G > kDecPrepIters * 4 * c.W) return false;
+  if (OUTmode == OUT_NORM && K / 8 > rows_xchunks(true) * 64 * c.W) return false;
+  c.lds = dec_lds_units(K, G, OUTmode == OUT_NORM, c.S, c.W, c.D) * 16;
+  const int per_wg = c.lds + dec_static_lds(c.S, c.W);
+  if (per_wg > kLdsBytes) return false;
+  const long long units = (long long)tiles * 4 / c.S;
+  // one workgroup per CU (gate|up: 256 workgroups 17.6 us, two per CU 19.1 us)
+  const long long cap = OUTmode == OUT_SWIGLU ? units / 2 : units;
+  const int tP = g_dec_tune.P.load(std::memory_order_relaxed);
+  c.P = (int)std::max<long long>(1, std::min(cap, tP > 0 ? (long long)tP : (long long)device_cus()));
+  return true;
+}
+
+template <int OUT, int I>
+void launch_dec_i(const SkinnyArgs& a, const DecCfg& c, hipStream_t st) {
+  constexpr DecVariant v = kDecAll[I];
+  constexpr auto kern = &k_dec<OUT, v.S, v.W, v.D>;
+  if (c.S == v.S && c.W == v.W && c.D == v.D) {
+    allow_lds<kern>(c.lds);
+    kern<<<a.P, 64 * v.W, c.lds, st>>>(a);
+    return;
+  }
+  if constexpr (I + 1 < (OUT == OUT_BF16 ? kDecCount : kDecPolicy)) launch_dec_i<OUT, I + 1>(a, c, st);
+}
+
+template <int OUT>
+void launch_dec(const SkinnyArgs& a, const DecCfg& c, hipStream_t st) {
+  launch_dec_i<OUT, 0>(a, c, st);
+}
+
+template <int OUT, int I>
+void prepare_dec_i() {
+  constexpr DecVariant v = kDecAll[I];
+  allow_lds<&k_dec<OUT, v.S, v.W, v.D>>(kLdsBytes - dec_static_lds(v.S, v.W));
+  if constexpr (I + 1 < (OUT == OUT_BF16 ? kDecCount : kDecPolicy)) prepare_dec_i<OUT, I + 1>();
+}
+
+template <int OUT>
+void prepare_dec() {
+  prepare_dec_i<OUT, 0>();
 }
 
 template <int OUT, int FMT, int S, int W, int D, bool XL>
@@ -1450,6 +1933,12 @@ void prepare_dma_lds() {
   static bool done[64] = {false};
   bool& d = done[current_device()];
   if (d) return;
+  prepare_dec<OUT_BF16>();
+  prepare_dec<OUT_F32>();
+  prepare_dec<OUT_ARGMAX>();
+  prepare_dec<OUT_RES>();
+  prepare_dec<OUT_SWIGLU>();
+  prepare_dec<OUT_NORM>();
   prepare_dma_out<OUT_BF16, 4>();
   prepare_dma_out<OUT_F32, 4>();
   prepare_dma_out<OUT_ARGMAX, 4>();
@@ -1540,12 +2029,15 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   // loads address weights and x through 32-bit buffer offsets
   if (w.weight_bytes >= (1ull << 32)) return QW4_ERR_SHAPE;
   const bool m1 = M == 1;
+  DecCfg dc{};
+  const int dmode = g_dec_tune.mode.load(std::memory_order_relaxed);
+  const bool use_dec = FMT == 4 && m1 && dmode != 1 && dec_config(w.out_f, w.G, OUT, dc);
   const Launch l = m1 ? launch_for<OUT, true, FMT>(w.out_f, w.G, M)
                       : launch_for<OUT, false, FMT>(w.out_f, w.G, M);
   if ((size_t)l.P * 2 * 1024 > slot_floats() ||
       slot_floats() + (size_t)tiles * 64 * 2 > s->partial_elems)
     return QW4_ERR_SCRATCH;
-  SkinnyArgs a;
+  SkinnyArgs a{};
   a.qw = static_cast<const uint32_t*>(w.qw);
   a.sc = w.sc;
   a.zr = w.zr;
@@ -1570,9 +2062,18 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.eps = e.eps;
   a.ld = OUT == OUT_SWIGLU ? w.out_f / 2 : w.out_f;
   if (OUT == OUT_SWIGLU && (w.out_f % (2 * kTileN))) return QW4_ERR_SHAPE;
-  if (OUT == OUT_NORM && !l.XL) return QW4_ERR_SHAPE;   // x must fit the LDS staging
   if (OUT == OUT_RES && !e.res) return QW4_ERR_NULL;
   if (OUT == OUT_NORM && (!e.nw || M > 16)) return QW4_ERR_NULL;
+  if constexpr (FMT == 4) {
+    if (use_dec) {
+      a.U = tiles * 4 / dc.S;
+      a.P = dc.P;
+      launch_dec<OUT>(a, dc, (hipStream_t)stream);
+      QW4_LAUNCH_CHECK();
+      return QW4_OK;
+    }
+  }
+  if (OUT == OUT_NORM && !l.XL) return QW4_ERR_SHAPE;   // x must fit the LDS staging
   if (l.S) {
     a.U = tiles * 4 / l.S;
     launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
@@ -1626,6 +2127,15 @@ int run_skinny8(void* y, const qw4_w8_weights* w, const uint16_t* x, int M, qw4_
 using namespace qw4;
 
 extern "C" {
+
+int qw4_tune_decode(int mode, int S, int W, int D, int P) {
+  g_dec_tune.mode.store(mode, std::memory_order_relaxed);
+  g_dec_tune.S.store(S, std::memory_order_relaxed);
+  g_dec_tune.W.store(W, std::memory_order_relaxed);
+  g_dec_tune.D.store(D, std::memory_order_relaxed);
+  g_dec_tune.P.store(P, std::memory_order_relaxed);
+  return QW4_OK;
+}
 
 int qw4_choose_splits(int out_f, int num_groups) {
   if (out_f < kTileN || num_groups <= 0) return 1;

@@ -7,7 +7,9 @@
 //       position p of a tile holds row  n = 4*(p % 16) + p / 16,
 //       word w of chunk j covers k = 128*g + 32*j + 8*w + e, e = 0..7,
 //       element e sits in nibble slot (e % 2) * 4 + e / 2.
-//   scale   bf16 [N/64][G][64]        natural row order inside the tile
+//   scale   u16  [N/64][G][80]        per (tile, group) one 160-byte record: the
+//                                     64 bf16 scales in natural row order, then
+//                                     a copy of the block's 16 zero-point words
 //   zeros   u16  [N/64][G][16]        u16 c holds rows 4c..4c+3, row 4c+t at bits 4t
 //
 // Why this shape:
@@ -21,6 +23,9 @@
 //     8-byte load, its zero points one u16, its outputs one 8-byte store.
 //   * the (tile, group) block is 4 KiB contiguous: the decode kernels stream
 //     it with 16-byte loads and the prefill GEMM stages it into LDS unchanged.
+//   * scales and zero points of a block sit in one 160-byte record, so the
+//     decode GEMV fetches both with one load per item (the zero points are
+//     also kept on their own for the other kernels).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -30,6 +35,8 @@ namespace qw4 {
 constexpr int kTileN = 64;          // output rows per tile
 constexpr int kGroup = 128;         // inputs per quantization group
 constexpr int kWordsPerBlock = 1024;  // u32 words per (tile, group)
+constexpr int kMetaU16 = 80;        // u16 per (tile, group) in the 4-bit scale array
+constexpr int kMetaBytes = 2 * kMetaU16;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));

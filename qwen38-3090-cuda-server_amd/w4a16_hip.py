@@ -169,6 +169,7 @@ def lib():
         "qw4_gemv_rmsnorm": ([vp, W, vp, vp, C.c_float, i, vp, S, vp], i),
         "qw4_linear": ([vp, W, vp, i, S, WS, vp], i),
         "qw4_linear_max_t": ([W], i),
+        "qw4_tune_decode": ([i, i, i, i, i], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -396,6 +397,13 @@ def linear_w4a16(y, w: W4A16Weights, x, T: int, s: GemvScratch, ws: GemmWorkspac
     _need(x, max(T, 0) * w.in_f * 2, "linear x")
     _chk(lib().qw4_linear(_ptr(y), C.byref(w), _ptr(x), T, C.byref(s),
                           C.byref(ws) if ws is not None else None, _stream(stream)), "linear")
+
+
+def tune_decode(mode: int = 0, S: int = 0, W: int = 0, D: int = 0, P: int = 0) -> None:
+    """Tuning and test override of the M = 1 decode launch (qw4_tune_decode):
+    mode 0 = the library's policy, 1 = k_rows, 2 = k_dec; S / W / D / P force
+    unit size, waves, item depth and workgroups (0 = policy)."""
+    _chk(lib().qw4_tune_decode(mode, S, W, D, P), "tune_decode")
 
 
 def linear_max_t(w: W4A16Weights) -> int:

@@ -56,7 +56,7 @@ def weights_buffers(w, N: int, K: int):
 
     G = K // 128
     out = []
-    for ptr, n in ((w.qweight, N * K // 2), (w.scale, N * G * 2), (w.zeros, N * G // 2)):
+    for ptr, n in ((w.qweight, N * K // 2), (w.scale, N * G * 5 // 2), (w.zeros, N * G // 2)):
         buf = torch.empty(n, dtype=torch.uint8, device="cuda")
         torch.cuda.synchronize()
         hipMemcpy = C.CDLL("libamdhip64.so").hipMemcpy
