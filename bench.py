@@ -205,29 +205,6 @@ class Bench:
         log(f"config2: {ms:.3f} ms/step, {value:.1f} GB/s")
         del g_step
 
-        # Per-projection launch duration: HIP does not allow timing events as
-        # graph nodes, so each projection's 64 launches are a graph of their
-        # own, timed with events on the launch stream (includes the ~1 us gap
-        # between consecutive kernels).
-        per_op, tot_ms, tot_bytes, launches = {}, 0.0, 0, 0
-        for li, (name, K, N) in enumerate(LAYER):
-            g1 = self.capture(lambda: [hip.gemv_w4a16(ys, lw[li], xs[K], scratch)
-                                       for lw in self.layers])
-            d = self.time_graph(g1, 3) / len(self.layers)
-            del g1
-            b = alg_bytes(1, K, N)
-            per_op[name] = {"K": K, "N": N, "us": round(d * 1e3, 2),
-                            "GBps": round(b / (d * 1e-3) / 1e9, 1),
-                            "splits": hip.gemv_choose_splits(N, K // 128)}
-            tot_ms += d * len(self.layers)
-            tot_bytes += b * len(self.layers)
-            launches += len(self.layers)
-        self.extra["kernel_timing"] = ("per-projection graphs of 64 launches, HIP events on the "
-                                       "launch stream (includes inter-kernel gaps)")
-        self.extra["config2_per_projection"] = per_op
-        self.extra["config2_launches_per_step"] = 4 * args.layers
-        self.extra["config2_kernel_only_GBps"] = round(tot_bytes / (tot_ms * 1e-3) / 1e9, 1)
-
         # ------------------------------------------------ HBM read microbench
         buf = torch.empty(4 << 30, dtype=torch.uint8, device="cuda")
         sink = torch.empty(8192, dtype=torch.int32, device="cuda")
@@ -243,6 +220,30 @@ class Bench:
         self.extra["measured_hbm_read_GBps"] = round(hbm, 1)
         self.extra["config2_frac_of_measured_hbm"] = round(value / hbm, 4)
         log(f"stream read {hbm:.1f} GB/s")
+
+        # Per-projection launch duration: HIP does not allow timing events as
+        # graph nodes, so each projection's 64 launches are a graph of their
+        # own, timed with events on the launch stream (includes the ~1 us gap
+        # between consecutive kernels).
+        per_op, tot_ms, tot_bytes, launches = {}, 0.0, 0, 0
+        for li, (name, K, N) in enumerate(LAYER):
+            g1 = self.capture(lambda: [hip.gemv_w4a16(ys, lw[li], xs[K], scratch)
+                                       for lw in self.layers])
+            d = self.time_graph(g1, 3) / len(self.layers)
+            del g1
+            b = alg_bytes(1, K, N)
+            per_op[name] = {"K": K, "N": N, "us": round(d * 1e3, 2),
+                            "GBps": round(b / (d * 1e-3) / 1e9, 1),
+                            "frac_of_measured_hbm": round(b / (d * 1e-3) / 1e9 / hbm, 4),
+                            "splits": hip.gemv_choose_splits(N, K // 128)}
+            tot_ms += d * len(self.layers)
+            tot_bytes += b * len(self.layers)
+            launches += len(self.layers)
+        self.extra["kernel_timing"] = ("per-projection graphs of 64 launches, HIP events on the "
+                                       "launch stream (includes inter-kernel gaps)")
+        self.extra["config2_per_projection"] = per_op
+        self.extra["config2_launches_per_step"] = 4 * args.layers
+        self.extra["config2_kernel_only_GBps"] = round(tot_bytes / (tot_ms * 1e-3) / 1e9, 1)
         avg_bytes, avg_ms = tot_bytes / launches, tot_ms / launches
         return {"value": value, "ms": ms, "step_bytes": step_bytes, "avg_bytes": avg_bytes,
                 "avg_ms": avg_ms}
@@ -444,9 +445,29 @@ class Bench:
             "frac_of_measured_hbm": round(agg / hbm, 4) if hbm else None}
         log(f"reference mix: {agg:.1f} GB/s, {tt / 1e3:.3f} ms/token")
 
+    def mfma_peak(self):
+        """Measured bf16 MFMA throughput (v_mfma_f32_32x32x16_bf16 chains on random
+        operands, 4096 workgroups of 4 waves), the prefill roofline's measured
+        denominator next to the published 2.5 PFLOP/s."""
+        hip, torch = self.hip, self.torch
+        sink = torch.empty(4096, dtype=torch.int32, device="cuda")
+        blocks, iters = 4096, 2000
+        hip.mfma_peak(sink, blocks, 200)
+        torch.cuda.synchronize()
+        a = self.T.event()
+        hip.mfma_peak(sink, blocks, iters)
+        b = self.T.event()
+        torch.cuda.synchronize()
+        fl = blocks * 4.0 * iters * 8 * 32768
+        tf = fl / (a.elapsed_time(b) * 1e-3) / 1e12
+        self.extra["measured_mfma_bf16_TFLOPS"] = round(tf, 1)
+        log(f"mfma peak {tf:.1f} TFLOP/s")
+        return tf
+
     # ---------------------------------------------------------- config 4
     def prefill(self):
         hip, torch = self.hip, self.torch
+        mpk = self.mfma_peak()
         c4 = {}
         A = torch.empty((4096, 17408), dtype=torch.int16, device="cuda")
         hip.gen_bf16(A, A.numel(), 0, 4242, 0)
@@ -481,6 +502,7 @@ class Bench:
         self.extra["roofline_prefill"] = {
             "bound": "mfma", "achieved": round(pf_tf, 1), "peak": BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s", "frac": round(pf_tf / BF16_PEAK_TFLOPS, 4),
+            "measured_peak": round(mpk, 1), "frac_of_measured_peak": round(pf_tf / mpk, 4),
             "traffic": traffic_from_profiles("k_gemm"),
             "kernel": "k_gemm (+ k_gemm_fixup when tiles are split), M=4096, gate 17408x5120 + "
                       "down 5120x17408"}
@@ -544,8 +566,8 @@ def main():
                      "achieved": round(d["avg_bytes"] / (d["avg_ms"] * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["avg_bytes"] / (d["avg_ms"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": traffic_from_profiles("k_rows_decode_sweep"),
-                     "kernel": "k_rows (decode GEMV), avg over the sweep's 4 shapes",
+                     "traffic": traffic_from_profiles("k_dec_decode_sweep"),
+                     "kernel": "k_dec (decode GEMV, integer MFMA), avg over the sweep's 4 shapes",
                      "alg_bytes_per_launch": round(d["avg_bytes"]),
                      "avg_launch_us": round(d["avg_ms"] * 1e3, 3)},
         "cpu_baseline": cpu,

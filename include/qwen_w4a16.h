@@ -116,6 +116,14 @@ int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
  * to occupy the chip; env QW4_SKINNY_W / QW4_SKINNY_S override, for tuning). */
 int qw4_choose_splits(int out_f, int num_groups);
 
+/* Tuning override of the M = 1 decode launch (no reference counterpart; for
+ * benchmarks and tests). mode 0: the library's measured policy; 1: the
+ * general skinny kernel (k_rows) instead of the integer-MFMA decode kernel;
+ * 3: the decode kernel with unit size S (row quads), W waves and D items in
+ * flight per wave (0 = the policy's value). P > 0 forces the workgroup count.
+ * Process-wide; set it between launches, not while other threads launch. */
+int qw4_tune_decode(int mode, int S, int W, int D, int P);
+
 /* ------------------------------------------------------- decode / verify
  * y [M][out_f] = x [M][in_f] @ W^T, bf16 row-major, fp32 accumulation.
  * x must be 16-byte aligned; y 8-byte aligned (16 for fp32).
@@ -301,6 +309,13 @@ int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_
  * reference's bench/microbench.cu "streaming read"): reads `bytes` (multiple of
  * 16) with 16-byte loads and writes one XOR per workgroup to sink[blocks]. */
 int qw4_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
+/* MFMA peak microbenchmark (no reference counterpart; the intent of the
+ * reference's bench/microbench.cu peak measurement, used as the measured
+ * denominator next to the published bf16 peak): `blocks` workgroups of 4
+ * waves, each wave `iters` x 8 v_mfma_f32_32x32x16_bf16 (32768 flop each) on
+ * random operands; writes one word per workgroup to sink[blocks]. */
+int qw4_mfma_peak(uint32_t* sink, int blocks, int iters, void* stream);
 
 #ifdef __cplusplus
 }

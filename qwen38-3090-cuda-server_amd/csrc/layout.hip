@@ -314,6 +314,38 @@ int check_weights_public(const qw4_weights* w) { return check_weights(w); }
 
 using namespace qw4;
 
+// MFMA peak microbenchmark: every wave runs `iters` rounds of 8 independent
+// v_mfma_f32_32x32x16_bf16 chains on operands hashed from the lane id (random
+// bits keep the matrix cores at their realistic power draw) and folds the
+// accumulators into sink[block] so nothing is dead code.
+__global__ __launch_bounds__(256) void k_mfma_peak(uint32_t* sink, int iters) {
+  typedef __bf16 bf16x8v __attribute__((ext_vector_type(8)));
+  const uint32_t l = threadIdx.x + 977u * blockIdx.x;
+  u32x4 ra, rb;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bf16 pairs in [1, 2): exponent fixed, mantissas hashed
+    ra[i] = 0x3F803F80u | ((l * 2654435761u + 40503u * i) & 0x007F007Fu);
+    rb[i] = 0x3F803F80u | ((l * 2246822519u + 91711u * i) & 0x007F007Fu);
+  }
+  const bf16x8v A = __builtin_bit_cast(bf16x8v, ra), B = __builtin_bit_cast(bf16x8v, rb);
+  f32x16 acc[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[k][e] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, B, acc[k], 0, 0, 0);
+  }
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v += acc[k][e];
+  if (threadIdx.x == 0) sink[blockIdx.x] = __float_as_uint(v);
+}
+
 extern "C" {
 
 const char* qw4_status_string(int st) {
@@ -520,6 +552,14 @@ int qw4_gen_awq_k(uint32_t* qweight, uint16_t* scales, uint32_t* zeros, int out_
   const size_t nm = (size_t)(in_f / kGroup) * (out_f / 8);
   k_gen_awq_k_meta<<<(unsigned)std::min<size_t>(blocks_for(nm, 256), 65536), 256, 0, hs>>>(
       scales, zeros, out_f, in_f / kGroup, seed, tensor);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_mfma_peak(uint32_t* sink, int blocks, int iters, void* stream) {
+  if (!sink) return QW4_ERR_NULL;
+  if (blocks <= 0 || iters <= 0) return QW4_ERR_SHAPE;
+  k_mfma_peak<<<blocks, 256, 0, (hipStream_t)stream>>>(sink, iters);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
 }

@@ -45,7 +45,7 @@ EXPORTS = (
     "qw4_w8_quantize", "qw4_w8_free", "qw4_w8_bytes", "qw4_w8_dequant_rows", "qw4_w8_gemv",
     "qw4_w8_gemm_small", "qw4_w8_gemv_argmax",
     "qw4_rmsnorm", "qw4_residual_add", "qw4_swiglu", "qw4_gemv_residual", "qw4_gemv_swiglu",
-    "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t",
+    "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t", "qw4_mfma_peak", "qw4_tune_decode",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -170,6 +170,7 @@ def lib():
         "qw4_linear": ([vp, W, vp, i, S, WS, vp], i),
         "qw4_linear_max_t": ([W], i),
         "qw4_tune_decode": ([i, i, i, i, i], i),
+        "qw4_mfma_peak": ([vp, i, i, vp], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -495,6 +496,12 @@ def gen_awq_k(qweight, scales, zeros, out_f: int, in_f: int, seed: int, tensor: 
     _need(zeros, G * out_f // 8 * 4, "gen_awq_k zeros")
     _chk(lib().qw4_gen_awq_k(_ptr(qweight), _ptr(scales), _ptr(zeros), out_f, in_f, seed,
                              tensor, _stream(stream)), "gen_awq_k")
+
+
+def mfma_peak(sink, blocks: int, iters: int, stream=None) -> None:
+    """MFMA microbenchmark: blocks x 4 waves x iters x 8 bf16 32x32x16 MFMAs."""
+    _need(sink, blocks * 4, "mfma_peak sink")
+    _chk(lib().qw4_mfma_peak(_ptr(sink), blocks, iters, _stream(stream)), "mfma_peak")
 
 
 def stream_read(src, nbytes: int, sink, blocks: int, stream=None) -> None:
