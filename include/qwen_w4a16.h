@@ -112,17 +112,28 @@ int qw4_scratch_free(qw4_scratch* s);
 /* gemv_partial_check (gemv_w4a16.cuh:109-110; .cu:359-366), as a status code. */
 int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
 /* gemv_choose_splits (gemv_w4a16.cuh:134; .cu:289-306): cross-workgroup
- * K-splits the skinny kernel uses for this shape (1 unless out_f is too small
- * to occupy the chip; env QW4_SKINNY_W / QW4_SKINNY_S override, for tuning). */
+ * K-splits the skinny kernels use for this shape. Always 1: every workgroup
+ * owns whole output rows over all of K (measured on MI355X, splitting lost at
+ * every shape: see the decode design notes). */
 int qw4_choose_splits(int out_f, int num_groups);
 
-/* Tuning override of the M = 1 decode launch (no reference counterpart; for
- * benchmarks and tests). mode 0: the library's measured policy; 1: the
- * general skinny kernel (k_rows) instead of the integer-MFMA decode kernel;
- * 3: the decode kernel with unit size S (row quads), W waves and D items in
- * flight per wave (0 = the policy's value). P > 0 forces the workgroup count.
- * Process-wide; set it between launches, not while other threads launch. */
+/* Tuning and test overrides (no reference counterpart; for benchmarks and
+ * tests; process-wide atomics, read at each launch: set them between launches).
+ * qw4_tune_decode, the skinny launches: mode 0 the library's measured policy;
+ * 1 the bf16 skinny kernel (k_rows) instead of the integer-MFMA decode kernel
+ * at M = 1, S (1, 2, 4 row quads per unit) and D (2..4) forcing its unit size
+ * and LDS-DMA depth; 2 k_rows with items in
+ * registers for every M, S (1, 2, 4 row quads per unit) and W (8, 16 waves)
+ * forcing its shape; 3 the decode kernel with unit size S, W waves and D items
+ * per wave (0 = the policy's value). P > 0 forces the decode kernel's
+ * workgroup count. */
 int qw4_tune_decode(int mode, int S, int W, int D, int P);
+/* qw4_tune_gemm: the prefill schedule, -1 the cost model (default), 0 one
+ * workgroup per tile, 1 stream-K, 2 hybrid (split schedules need a workspace). */
+int qw4_tune_gemm(int schedule);
+/* qw4_tune_linear: max_t of qw4_linear for every weight, 0 = the measured rule
+ * (the role of the reference's QWEN_MMA_MAX_T environment variable). */
+int qw4_tune_linear(int max_t);
 
 /* ------------------------------------------------------- decode / verify
  * y [M][out_f] = x [M][in_f] @ W^T, bf16 row-major, fp32 accumulation.
@@ -220,7 +231,7 @@ int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
  * x through the GEMV (T = 1), the skinny kernel in chunks of up to 16 rows
  * (2 <= T <= max_t), or the prefill GEMM (T > max_t). max_t is the crossover
  * measured on MI355X for this weight's size (qw4_linear_max_t: 48 rows for
- * a 93 MB projection, 112 for an 11 MB one); env QW4_LIN_MAX_T overrides it,
+ * a 93 MB projection, 112 for an 11 MB one); qw4_tune_linear overrides it,
  * as QWEN_MMA_MAX_T does in the reference. ws may be NULL. */
 int qw4_linear(uint16_t* y, const qw4_weights* w, const uint16_t* x, int T, qw4_scratch* s,
                qw4_workspace* ws, void* stream);

@@ -10,6 +10,9 @@
 // workspace is given; the workspace then holds fp32 partial tiles.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <mutex>
+
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -437,17 +440,22 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
 size_t gemm_workspace_need(int cus) { return 2ull * (size_t)cus * kSlotBytes; }
 
 int device_cus() {
-  static int cached[64] = {0};
+  static std::once_flag once[64];
+  static int cus[64];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
+  std::call_once(once[dev], [dev] {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
       n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
+    cus[dev] = n;
+  });
+  return cus[dev];
 }
+
+// Tuning and test override of the prefill schedule (qw4_tune_gemm): -1 the
+// cost model, 0 per tile, 1 stream-K, 2 hybrid.
+std::atomic<int> g_gemm_schedule{-1};
 
 }  // namespace
 }  // namespace qw4
@@ -478,6 +486,12 @@ int qw4_workspace_free(qw4_workspace* ws) {
   return QW4_OK;
 }
 
+int qw4_tune_gemm(int schedule) {
+  if (schedule < -1 || schedule > 2) return QW4_ERR_SHAPE;
+  g_gemm_schedule.store(schedule, std::memory_order_relaxed);
+  return QW4_OK;
+}
+
 int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_workspace* ws,
              void* stream) {
   int st = check_weights_public(w);
@@ -491,13 +505,9 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
   {
     const int tiles_n = (w->out_f + G2_BN - 1) / G2_BN;
     const int tiles_m = (M + G2_BM - 1) / G2_BM;
-    static const int map_env = [] {
-      const char* e = std::getenv("QW4_GEMM_MAP");
-      return e ? std::atoi(e) : 1;
-    }();
     const int nt = tiles_n * tiles_m;
     GemmArgs a{w->qweight, w->scale, w->zeros, A, C, nullptr, M, w->out_f, w->in_f,
-                w->num_groups, tiles_n, tiles_m, map_env && nt % 8 == 0, nt, nt, 0};
+                w->num_groups, tiles_n, tiles_m, nt % 8 == 0, nt, nt, 0};
     int grid = nt;
     // Three schedules, costed in group-steps per CU (one 256 x 256 x 128
     // tile step; measured on MI355X at the config-4 shapes):
@@ -509,10 +519,9 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     //  * hybrid: whole tiles for the floor(nt / CUs) full rounds, then the
     //    other nt % CUs tiles split over the CUs: the same work, one partial
     //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile.
-    // A split schedule runs when it beats per-tile by 10%. QW4_GEMM_SK: 0
-    // never splits, 1 forces stream-K, 2 the hybrid (read on every call).
-    const char* ske = std::getenv("QW4_GEMM_SK");
-    const int sk_env = ske ? std::atoi(ske) : -1;
+    // A split schedule runs when it beats per-tile by 10% (qw4_tune_gemm
+    // forces one, for tests and tuning).
+    const int sk_env = g_gemm_schedule.load(std::memory_order_relaxed);
     const int cus = device_cus();
     const long long G = w->num_groups;
     const int rem = nt % cus;
@@ -540,18 +549,12 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
       a.map = 1;
       grid = cus;
     }
-    static const int nh = [] {
-      const char* e = std::getenv("QW4_GEMM_NH");
-      return e ? std::atoi(e) : 1;
-    }();
     hipStream_t s = (hipStream_t)stream;
-    if (nh == 2) k_gemm<2><<<grid, 512, 0, s>>>(a);
-    else k_gemm<1><<<grid, 512, 0, s>>>(a);
+    k_gemm<1><<<grid, 512, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
     if (a.full != nt) {   // the split tiles
       const int fb = (nt - a.full) * G2_WAVES * kFixParts;
-      if (nh == 2) k_gemm_fixup<2><<<fb, 64, 0, s>>>(a);
-      else k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
+      k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;

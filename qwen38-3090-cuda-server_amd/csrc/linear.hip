@@ -2,11 +2,13 @@
 // :643-658) over this library's kernels: the GEMV for one row, the skinny
 // kernel in chunks of up to 16 rows while it reads the weights fewer times
 // than the prefill GEMM would cost, the prefill GEMM beyond. Host code only.
-#include <cstdlib>
+#include <atomic>
 
 #include "../../include/qwen_w4a16.h"
 
 namespace {
+
+std::atomic<int> g_lin_max_t{0};   // qw4_tune_linear override (0: the rule below)
 
 // Rows up to which 16-row skinny passes beat the prefill GEMM. Measured on
 // MI355X over the model's projections (T = 16 .. 256): a skinny pass costs
@@ -15,8 +17,7 @@ namespace {
 // under their ratio -- 48 rows for gate|up (93 MB; measured ~55), 64 for down
 // (46 MB; ~60), 96 for qkv (19 MB; ~107), 112 for o_proj (11 MB; ~127).
 int lin_max_t(const qw4_weights* w) {
-  const char* e = std::getenv("QW4_LIN_MAX_T");
-  const int v = e ? std::atoi(e) : 0;
+  const int v = g_lin_max_t.load(std::memory_order_relaxed);
   if (v > 0) return v;
   const double mb = (double)w->out_f * w->in_f * (0.5 + 2.5 / 128) / 1e6;
   const int chunks = (int)((60.0 + 0.4 * mb) / (0.245 * mb + 5.8));
@@ -26,6 +27,12 @@ int lin_max_t(const qw4_weights* w) {
 }  // namespace
 
 extern "C" {
+
+int qw4_tune_linear(int max_t) {
+  if (max_t < 0) return QW4_ERR_SHAPE;
+  g_lin_max_t.store(max_t, std::memory_order_relaxed);
+  return 0;
+}
 
 int qw4_linear_max_t(const qw4_weights* w) {
   if (!w || w->out_f <= 0 || w->in_f <= 0) return QW4_ERR_NULL;

@@ -1,11 +1,17 @@
 // Decode GEMV (M = 1), speculative-verify skinny GEMM (M = 2..16) and the
-// lm_head GEMV with a fused fp32 row-argmax: two gfx950 kernels over the same
-// per-block math.
+// lm_head GEMV with a fused fp32 row-argmax: two gfx950 kernels.
 //
-// Math. A 64-row tile of packed weights is split into 4 KiB (tile, group)
-// blocks (4-bit; 8 KiB for 8-bit weights). Lane c + 16q of a wave reads chunk
-// q of positions 16 st + c, i.e. rows 4c + st, and feeds bf16 MFMA
-// v_mfma_f32_16x16x32_bf16:
+// k_dec (M = 1, 4-bit weights, every epilogue): integer MFMA. Each 128-group
+// of x becomes exact 3-byte fixed point (int8 rows of the A operand of
+// v_mfma_i32_16x16x64_i8), the packed nibbles are masked into int8 B operands
+// (3 VALU per word), and the zero point and scale are applied per row and
+// group in int32 / fp32. Items (one group of a 32-row unit: 2 KiB of weights
+// plus a 160-byte scale/zero-point record) stream into per-wave LDS slots.
+//
+// k_rows (M > 1, the 8-bit head, and M = 1 shapes k_dec does not take): bf16
+// MFMA. A 64-row tile of packed weights is split into 4 KiB (tile, group)
+// blocks (8 KiB for 8-bit weights). Lane c + 16q of a wave reads chunk q of
+// positions 16 st + c, i.e. rows 4c + st, and feeds v_mfma_f32_16x16x32_bf16:
 //    A = activations, 16 rows (rows >= M unused), 32 k per instruction
 //    B = the packed word turned into 8 bf16 values (128 + q) by AND-OR
 // Four instructions per row quad st cover the group; a fifth B operand of ones
@@ -15,36 +21,15 @@
 // (the reference's identity, src/kernels/gemv_w4a16.cuh:25-37, with the group
 // sum computed by the matrix core instead of a prologue kernel).
 //
-// k_rows (default). Data-parallel: a workgroup owns whole units (S row quads
-// of a tile over all of K), its W waves split K and are summed in LDS in wave
-// order; no workgroup exchanges partials with another, so a launch ends when
-// its loads end. Items (one group of one unit) are loaded D ahead, either
-// into registers or -- the default -- straight into per-wave LDS slots
-// (buffer_load ... lds), which bounds the depth by LDS instead of registers.
-// M = 1 stages x in LDS once per workgroup. Epilogues: bf16 / fp32 output,
-// residual add, swiglu of gate|up pairs, rmsnorm of x in LDS before the
-// projection, and the fused argmax.
+// Both are data-parallel: a workgroup owns whole units (S row quads of a tile
+// over all of K), its waves split K and are summed in LDS in wave order; no
+// workgroup exchanges partials with another, so a launch ends when its loads
+// end and every output is bitwise reproducible (the property of
+// gemv_w4a16.cu:262-279). Epilogues: bf16 / fp32 output, residual add, swiglu
+// of gate|up pairs, rmsnorm of x in LDS before the projection, and the fused
+// argmax.
 //
-// k_skinny (QW4_ROWS = 0). Stream-K: a fixed number of workgroups P sized to
-// the chip cuts the flattened list of U = tiles x groups blocks into P equal
-// contiguous ranges; a tile cut by a range boundary ("split tile") is
-// finished by whichever contributor completes it last:
-//  * M = 1: each contributor adds its partial, as 2^-20 fixed point biased by
-//    2^49, into one 64-bit word per output element with a returning
-//    device-scope atomic, together with 1 << 56 as an arrival count. Integer
-//    addition is order-independent (bitwise deterministic), and the contributor
-//    whose add completes the count holds the exact total in the returned value,
-//    rounds it once and emits it, then clears the word. Limits: |partial| <
-//    2^29 and at most 64 contributors per tile (ranges are kept >= G/60 blocks).
-//  * M > 1: each contributor writes its partial through (16-byte sc1 buffer
-//    stores) to its slot, waits for completion once at the end of the
-//    workgroup, then bumps the tile's counter (one per 128-byte line); the last
-//    one reads all slots back (sc1 loads) in workgroup order and emits.
-// Counters and words reset themselves, so the next call -- or a graph replay --
-// starts from zero. Both kernels sum in a fixed order, so every output is
-// bitwise reproducible (the property of gemv_w4a16.cu:262-279).
-//
-// Output layout per lane: acc[st][jj] is row m = 4q + jj, column
+// Output layout per lane (k_rows): acc[st][jj] is row m = 4q + jj, column
 // n = 64*tile + 4c + st.
 #include <hip/hip_runtime.h>
 
@@ -66,8 +51,7 @@ int check_weights_public(const qw4_weights* w);
 
 namespace {
 
-// Epilogues of the skinny kernels (k_rows takes every mode, k_skinny the
-// first three):
+// Epilogues of the skinny kernels:
 //   OUT_BF16   y = bf16(acc)
 //   OUT_F32    y = acc
 //   OUT_ARGMAX the row argmax of acc (no logits written)
@@ -81,14 +65,6 @@ enum { OUT_BF16 = 0, OUT_F32 = 1, OUT_ARGMAX = 2, OUT_RES = 3, OUT_SWIGLU = 4, O
 // Memory-side atomics on one cache line serialize; each counter gets its own line.
 constexpr int kCounterStride = 32;
 constexpr int kKeyGroups = 64;
-// The most workgroups per CU a scratch buffer is sized for.
-constexpr int kMaxWgsPerCu = 8;
-
-// Fixed-point split-tile accumulation (M = 1).
-constexpr float kFixScale = 1048576.0f;   // 2^20 (exact scaling)
-constexpr long long kFixBias = 1LL << 49;
-constexpr uint64_t kFixCount = 1ull << 56;
-constexpr uint64_t kFixMask = kFixCount - 1;
 
 struct SkinnyArgs {
   const uint32_t* qw;
@@ -96,15 +72,11 @@ struct SkinnyArgs {
   const uint16_t* zr;
   const uint16_t* x;
   void* y;
-  float* slots;         // M > 1: [P][2][4 st][64 lanes] f32x4 partials
-  uint64_t* sums;       // M = 1: [tiles][64 columns] accumulators
   uint32_t* counters;   // one counter per 128-byte line (kCounterStride words):
-                        //   [0, max_tiles)        split-tile arrival (M > 1)
                         //   [max_tiles, +64)      argmax arrival, per key group
                         //   [max_tiles + 64]      argmax arrival, of key groups
   uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
   int M, N, K, G, tiles, max_tiles, P, U;
-  uint32_t slot_bytes;
   uint32_t weight_bytes;   // packed weights (4- or 8-bit blocks)
   const uint16_t* res;     // OUT_RES: residual [M][N] (may be y)
   const uint16_t* nw;      // OUT_NORM: rmsnorm weight [K] (applied as 1 + w)
@@ -128,33 +100,10 @@ __device__ __forceinline__ void clear_dev(uint32_t* p) {
 // Wait until every memory operation this wave issued has completed.
 __device__ __forceinline__ void wait_all_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
-// 16-byte device-coherent (sc1) accesses to the slot buffer (M > 1).
-constexpr int kCpolSc1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t slot_rsrc(const SkinnyArgs& a) {
-  return __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)a.slot_bytes, 0x00020000);
-}
-__device__ __forceinline__ void st_slot(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCpolSc1);
-}
-__device__ __forceinline__ f32x4 ld_slot(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSc1));
-}
-
-// Stream-K range arithmetic: workgroup p owns blocks [start(p), start(p+1)).
+// Workgroup p owns units [start(p), start(p + 1)).
 __device__ __forceinline__ int range_start(const SkinnyArgs& a, int p) {
   return (int)((long long)p * a.U / a.P);
 }
-// Largest p with range_start(p) <= u.
-__device__ __forceinline__ int owner_of(const SkinnyArgs& a, int u) {
-  return (int)(((long long)(u + 1) * a.P - 1) / a.U);
-}
-
-struct GroupData {
-  u32x4 w[4];   // row quad st -> 4 words (k chunks t = 0..3)
-  u32x4 x[4];   // activation row c, k chunk t: 8 bf16
-  u32x2 s;      // scales of rows 4c..4c+3
-  uint32_t z;   // zero points of rows 4c..4c+3 (4 bits each)
-};
 
 // Buffer-resource loads: a loop-invariant per-lane offset plus a wave-uniform
 // scalar offset per block. Activation rows past M lie outside the x resource
@@ -181,48 +130,6 @@ __device__ __forceinline__ SkinnyRsrc skinny_rsrc(const SkinnyArgs& a) {
   return r;
 }
 
-// xoff: this lane's byte offset into x (row c, k chunk q; out of range for
-// c >= M). woff: its offset inside a 4 KiB block (chunk q, position c).
-__device__ __forceinline__ void load_group(GroupData& d, const SkinnyRsrc& r, const SkinnyArgs& a,
-                                           int b, int g, int c, uint32_t woff, uint32_t xoff) {
-  const uint32_t blk = (uint32_t)b * (uint32_t)a.G + (uint32_t)g;
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-    d.w[st] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + st * 256, blk * 4096u, 0);
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-    d.x[t] = __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
-  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * (uint32_t)kMetaBytes, 0);
-  d.z = __builtin_amdgcn_raw_buffer_load_b16(r.zr, (uint32_t)c * 2u, blk * 32u, 0);
-}
-
-__device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, NibConst k) {
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
-                                                       0x3F803F80u, 0x3F803F80u});
-  f32x4 C[4], Cs;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const bf16x8 A = __builtin_bit_cast(bf16x8, d.x[t]);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const bf16x8 B = nib8(d.w[st][t], k);
-      C[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          A, B, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : C[st], 0, 0, 0);
-    }
-    Cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones,
-                                                 t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Cs,
-                                                 0, 0, 0);
-  }
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const uint32_t sbits = (st & 1) ? (d.s[st >> 1] >> 16) : (d.s[st >> 1] & 0xffffu);
-    const float sf = bf16_bits_to_f32(sbits);
-    const float zf = 128.0f + (float)((d.z >> (4 * st)) & 0xFu);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) acc[st][jj] += sf * (C[st][jj] - zf * Cs[jj]);
-  }
-}
-
 // ------------------------------------------------------- 8-bit weights
 // W8A16 (the reference's lm_head format, gemv_w4a16.cuh:141-166): per (row,
 // 128-group) a bf16 scale and int8 q in [-127, 127], stored as the byte
@@ -231,28 +138,6 @@ __device__ __forceinline__ void mma_group(f32x4 (&acc)[4], const GroupData& d, N
 // k = 128 g + 32 j + [0, 32) in natural byte order. A byte is an exact bf16
 // (u <= 255 needs 8 significant bits); the offset is removed like the 4-bit
 // zero point: acc += s (C - 128 S_m), with S_m from the ones operand.
-struct GroupData8 {
-  u32x4 w[4][2];   // row quad st -> 32 bytes (k 32q .. 32q + 31)
-  u32x4 x[4];
-  u32x2 s;
-};
-
-__device__ __forceinline__ void load_group8(GroupData8& d, const SkinnyRsrc& r,
-                                            const SkinnyArgs& a, int b, int g, int c,
-                                            uint32_t woff, uint32_t xoff) {
-  const uint32_t blk = (uint32_t)b * (uint32_t)a.G + (uint32_t)g;
-#pragma unroll
-  for (int st = 0; st < 4; ++st)
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      d.w[st][h] = __builtin_amdgcn_raw_buffer_load_b128(r.qw, woff + st * 512 + h * 16,
-                                                         blk * 8192u, 0);
-#pragma unroll
-  for (int t = 0; t < 4; ++t)
-    d.x[t] = __builtin_amdgcn_raw_buffer_load_b128(r.x, xoff + t * 16, (uint32_t)g * 256u, 0);
-  d.s = __builtin_amdgcn_raw_buffer_load_b64(r.sc, (uint32_t)c * 8u, blk * 128u, 0);
-}
-
 // Eight bytes -> eight bf16 values (exact).
 __device__ __forceinline__ bf16x8 bytes8_bf16(uint32_t lo, uint32_t hi) {
   u32x4 o;
@@ -263,55 +148,13 @@ __device__ __forceinline__ bf16x8 bytes8_bf16(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8, o);
 }
 
-__device__ __forceinline__ void mma_group8(f32x4 (&acc)[4], const GroupData8& d) {
-  const bf16x8 ones = __builtin_bit_cast(bf16x8, u32x4{0x3F803F80u, 0x3F803F80u,
-                                                       0x3F803F80u, 0x3F803F80u});
-  f32x4 C[4], Cs;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const bf16x8 A = __builtin_bit_cast(bf16x8, d.x[t]);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const u32x4 v = d.w[st][t >> 1];
-      const bf16x8 B = bytes8_bf16(v[(t & 1) * 2], v[(t & 1) * 2 + 1]);
-      C[st] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-          A, B, t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : C[st], 0, 0, 0);
-    }
-    Cs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A, ones,
-                                                 t == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : Cs,
-                                                 0, 0, 0);
-  }
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const uint32_t sbits = (st & 1) ? (d.s[st >> 1] >> 16) : (d.s[st >> 1] & 0xffffu);
-    const float sf = bf16_bits_to_f32(sbits);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) acc[st][jj] += sf * (C[st][jj] - 128.0f * Cs[jj]);
-  }
-}
-
-// The two block formats behind one kernel.
+// Lane offset of its 16-byte chunk inside a block, per weight format: chunk
+// q of position c (4-bit: 1 KiB per chunk; 8-bit: 2 KiB, two 16-byte halves).
 template <int FMT>
-struct Fmt;
-template <>
-struct Fmt<4> {
-  using Data = GroupData;
-  __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 1024 + c * 16); }
-  __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
-                              int c, uint32_t woff, uint32_t xoff) {
-    load_group(d, r, a, b, g, c, woff, xoff);
+struct Fmt {
+  __device__ static uint32_t woff(int q, int c) {
+    return FMT == 8 ? (uint32_t)(q * 2048 + c * 32) : (uint32_t)(q * 1024 + c * 16);
   }
-  __device__ static void mma(f32x4 (&acc)[4], const Data& d, NibConst k) { mma_group(acc, d, k); }
-};
-template <>
-struct Fmt<8> {
-  using Data = GroupData8;
-  __device__ static uint32_t woff(int q, int c) { return (uint32_t)(q * 2048 + c * 32); }
-  __device__ static void load(Data& d, const SkinnyRsrc& r, const SkinnyArgs& a, int b, int g,
-                              int c, uint32_t woff, uint32_t xoff) {
-    load_group8(d, r, a, b, g, c, woff, xoff);
-  }
-  __device__ static void mma(f32x4 (&acc)[4], const Data& d, NibConst) { mma_group8(acc, d); }
 };
 
 // ------------------------------------------------------------- epilogues
@@ -335,128 +178,6 @@ __device__ __forceinline__ void best_fold(Best& bs, int jj, float v, int n) {
     bs.v[jj] = v;
     bs.n[jj] = n;
   }
-}
-
-// Final values of tile b (wave 0 of the finishing workgroup): store them, or
-// fold them into the workgroup's running argmax (lowest column on ties).
-template <int OUT>
-__device__ __forceinline__ void emit_tile(const SkinnyArgs& a, int b, const f32x4 (&acc)[4],
-                                          int lane, Best& bs) {
-  const int c = lane & 15, q = lane >> 4;
-  const int n0 = b * kTileN + 4 * c;
-  if (OUT == OUT_BF16) {
-    uint16_t* y = static_cast<uint16_t*>(a.y);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int m = 4 * q + jj;
-      if (m < a.M)
-        *reinterpret_cast<u32x2*>(y + (size_t)m * a.N + n0) =
-            u32x2{pack_bf16x2(acc[0][jj], acc[1][jj]), pack_bf16x2(acc[2][jj], acc[3][jj])};
-    }
-  } else if (OUT == OUT_F32) {
-    float* y = static_cast<float*>(a.y);
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int m = 4 * q + jj;
-      if (m < a.M)
-        *reinterpret_cast<f32x4*>(y + (size_t)m * a.N + n0) =
-            f32x4{acc[0][jj], acc[1][jj], acc[2][jj], acc[3][jj]};
-    }
-  } else {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-      for (int st = 0; st < 4; ++st) best_fold(bs, jj, acc[st][jj], n0 + st);
-  }
-}
-
-// M = 1: add this workgroup's partials of split tiles b0 (if h0) and b1 (if h1)
-// -- rows m = 0, held by lanes q = 0 in acc[st][0] -- and emit every element
-// this workgroup completes. All atomics are issued before any result is used.
-template <int OUT>
-__device__ __forceinline__ void fix_add_emit(const SkinnyArgs& a, int lane, Best& bs, int b0,
-                                             const f32x4 (&acc0)[4], bool h0, int b1,
-                                             const f32x4 (&acc1)[4], bool h1) {
-  const int c = lane & 15, q = lane >> 4;
-  if (q != 0) return;
-  uint64_t tot[2][4], add[2][4];
-  uint64_t* w[2][4];
-  const int bb[2] = {b0, b1};
-  const bool hh[2] = {h0, h1};
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (!hh[i]) continue;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      long long f = __float2ll_rn((i ? acc1[st][0] : acc0[st][0]) * kFixScale);
-      f = f > kFixBias - 1 ? kFixBias - 1 : (f < 1 - kFixBias ? 1 - kFixBias : f);
-      add[i][st] = kFixCount + (uint64_t)(f + kFixBias);
-      w[i][st] = a.sums + (size_t)bb[i] * 64 + 4 * c + st;
-      tot[i][st] = __hip_atomic_fetch_add(w[i][st], add[i][st], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    if (!hh[i]) continue;
-    const uint64_t S =
-        (uint64_t)(owner_of(a, bb[i] * a.G + a.G - 1) - owner_of(a, bb[i] * a.G) + 1);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const uint64_t t = tot[i][st] + add[i][st];
-      if ((t >> 56) == S) {
-        const long long v = (long long)(t & kFixMask) - (long long)S * kFixBias;
-        __hip_atomic_store(w[i][st], (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        // one rounding: int64 -> fp32, then an exact power-of-two scale
-        const float val = (float)v * (1.0f / kFixScale);
-        const int n = bb[i] * kTileN + 4 * c + st;
-        if (OUT == OUT_BF16)
-          static_cast<uint16_t*>(a.y)[n] = to_bf16(val);
-        else if (OUT == OUT_F32)
-          static_cast<float*>(a.y)[n] = val;
-        else
-          best_fold(bs, 0, val, n);
-      }
-    }
-  }
-}
-
-// M > 1: write this workgroup's partial of split tile b through to its slot
-// (0: the tile is its first, 1: its last).
-__device__ __forceinline__ void slot_store(const SkinnyArgs& a, int p, bool first_tile,
-                                           const f32x4 (&acc)[4], int lane) {
-  const int q = lane >> 4;
-  if (4 * q >= a.M) return;   // lanes holding only rows m >= M
-  const __amdgpu_buffer_rsrc_t r = slot_rsrc(a);
-  const uint32_t off = (uint32_t)((p * 2 + (first_tile ? 0 : 1)) * 4096 + lane * 16);
-#pragma unroll
-  for (int st = 0; st < 4; ++st) st_slot(r, off + st * 1024, acc[st]);
-}
-
-// M > 1, after this workgroup's slots are complete: count it in for tile b;
-// the last contributor sums the slots in workgroup order p0..p1 and emits.
-template <int OUT>
-__device__ __forceinline__ void slot_arrive(const SkinnyArgs& a, int b, int lane, Best& bs) {
-  const int p0 = owner_of(a, b * a.G), p1 = owner_of(a, b * a.G + a.G - 1);
-  uint32_t old = 0;
-  if (lane == 0) old = inc_dev(&a.counters[b * kCounterStride]);
-  old = __shfl(old, 0, 64);
-  if (old != (uint32_t)(p1 - p0)) return;
-  const int q = lane >> 4;
-  const __amdgpu_buffer_rsrc_t r = slot_rsrc(a);
-  f32x4 acc[4];
-#pragma unroll
-  for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (4 * q < a.M) {
-    for (int pp = p0; pp <= p1; ++pp) {
-      const int slot = (pp == p0 && range_start(a, pp) / a.G != b) ? 1 : 0;
-      const uint32_t off = (uint32_t)((pp * 2 + slot) * 4096 + lane * 16);
-#pragma unroll
-      for (int st = 0; st < 4; ++st) acc[st] += ld_slot(r, off + st * 1024);
-    }
-  }
-  if (lane == 0) clear_dev(&a.counters[b * kCounterStride]);
-  emit_tile<OUT>(a, b, acc, lane, bs);
 }
 
 // Wave 0 at the end of an argmax workgroup: fold the workgroup's best per row
@@ -508,101 +229,6 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
       clear_dev(done);
     }
   }
-}
-
-// ----------------------------------------------------------------- kernel
-// W waves per workgroup; M1: the fixed-point exchange (M = 1) or the slot
-// exchange (M > 1). Inside a tile segment each wave takes groups lo + wave,
-// lo + wave + W, ... in batches of two blocks (one for W = 16, to fit 128
-// VGPRs). W = 4: LDS sums double-buffered per segment; W >= 8: one buffer and
-// a second barrier.
-template <int OUT, int W, bool M1, int FMT>
-__global__ __launch_bounds__(64 * W) void k_skinny(SkinnyArgs a) {
-  constexpr int kNbuf = W == 4 ? 2 : 1;
-  constexpr int kBatch = W == 16 ? 1 : 2;
-  __shared__ f32x4 red[kNbuf][W - 1][4][64];
-  __shared__ f32x4 stash[4][64];   // M = 1: the first split tile's sums
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int c = lane & 15, q = lane >> 4;
-  const SkinnyRsrc rs = skinny_rsrc(a);
-  const uint32_t woff = Fmt<FMT>::woff(q, c);
-  const uint32_t xoff = (uint32_t)(c * a.K + 32 * q) * 2u;
-  const int p = blockIdx.x;
-  const int u0 = range_start(a, p), u1 = range_start(a, p + 1);
-  if (u0 >= u1) return;   // whole workgroup: no work
-  const int bfirst = u0 / a.G, blast = (u1 - 1) / a.G;
-  const int lo_first = u0 - bfirst * a.G;
-  const int hi_last = u1 - blast * a.G;
-  const NibConst k = nib_const();
-
-  int par = 0;
-  bool split_first = false, split_last = false;   // wave 0
-  f32x4 last_acc[4];
-  Best bs;
-  best_init(bs);
-  for (int sb = bfirst; sb <= blast; ++sb) {
-    const int lo = sb == bfirst ? lo_first : 0;
-    const int hi = sb == blast ? hi_last : a.G;
-    f32x4 acc[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) acc[st] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int g = lo + wave; g < hi; g += kBatch * W) {
-      typename Fmt<FMT>::Data d0, d1;
-      const bool two = kBatch == 2 && g + W < hi;
-      Fmt<FMT>::load(d0, rs, a, sb, g, c, woff, xoff);
-      if (two) Fmt<FMT>::load(d1, rs, a, sb, g + W, c, woff, xoff);
-      Fmt<FMT>::mma(acc, d0, k);
-      if (two) Fmt<FMT>::mma(acc, d1, k);
-    }
-    // Sum the segment over the W waves in wave order.
-    if (wave) {
-#pragma unroll
-      for (int st = 0; st < 4; ++st) red[par][wave - 1][st][lane] = acc[st];
-    }
-    __syncthreads();
-    if (wave == 0) {
-      for (int w = 0; w < W - 1; ++w)
-#pragma unroll
-        for (int st = 0; st < 4; ++st) acc[st] += red[par][w][st][lane];
-      if (lo == 0 && hi == a.G) {
-        emit_tile<OUT>(a, sb, acc, lane, bs);
-      } else if (sb == bfirst) {
-        split_first = true;
-        if (M1) {
-#pragma unroll
-          for (int st = 0; st < 4; ++st) stash[st][lane] = acc[st];
-        } else {
-          slot_store(a, p, true, acc, lane);
-        }
-      } else {
-        split_last = true;
-        if (M1) {
-#pragma unroll
-          for (int st = 0; st < 4; ++st) last_acc[st] = acc[st];
-        } else {
-          slot_store(a, p, false, acc, lane);
-        }
-      }
-    }
-    if (kNbuf == 2)
-      par ^= 1;
-    else
-      __syncthreads();   // red is reused by the next segment
-  }
-  if (wave == 0 && (split_first || split_last)) {
-    if (M1) {
-      f32x4 first_acc[4];
-#pragma unroll
-      for (int st = 0; st < 4; ++st) first_acc[st] = stash[st][lane];
-      fix_add_emit<OUT>(a, lane, bs, bfirst, first_acc, split_first, blast, last_acc,
-                        split_last);
-    } else {
-      wait_all_mem();   // slots complete before they are counted
-      if (split_first) slot_arrive<OUT>(a, bfirst, lane, bs);
-      if (split_last) slot_arrive<OUT>(a, blast, lane, bs);
-    }
-  }
-  if (OUT == OUT_ARGMAX && wave == 0) argmax_arrive(a, p, bs, lane);
 }
 
 // ------------------------------------------------------ data-parallel rows
@@ -1511,66 +1137,47 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
 }
 
 // ------------------------------------------------------------- host side
-// Workgroups per CU: the kernel's occupancy (all workgroups resident in one
-// round, equal work each). QW4_SKINNY_WGS_PER_CU, QW4_SKINNY_W (4|8|16) and
-// QW4_SKINNY_WG_TILES (tiles x 4 / n workgroups) override it, for tuning only.
-int g_env_wgs = 0, g_env_tiles_per_wg = 0, g_env_w = 0;
-std::once_flag g_env_once;
-int g_cus[64] = {0};
-int g_occ[64][3][3][2][2] = {{{{{0}}}}};
-
-void read_env() {
-  std::call_once(g_env_once, [] {
-    const char* e = std::getenv("QW4_SKINNY_WGS_PER_CU");
-    const int v = e ? std::atoi(e) : 0;
-    g_env_wgs = (v >= 1 && v <= kMaxWgsPerCu) ? v : 0;
-    const char* t = std::getenv("QW4_SKINNY_WG_TILES");
-    g_env_tiles_per_wg = t ? std::atoi(t) : 0;
-    const char* w = std::getenv("QW4_SKINNY_W");
-    g_env_w = w ? std::atoi(w) : 0;
-  });
-}
+// Per-device caches are filled once per device under std::call_once, or are
+// atomics whose racing writers store the same value; no launch reads the
+// environment.
+constexpr int kMaxDevices = 64;
 
 int current_device() {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = 0;
   return dev;
 }
 
 int device_cus() {
+  static std::once_flag once[kMaxDevices];
+  static int cus[kMaxDevices];
   const int dev = current_device();
-  if (!g_cus[dev]) {
+  std::call_once(once[dev], [dev] {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    g_cus[dev] = n;
-  }
-  return g_cus[dev];
+    cus[dev] = n;
+  });
+  return cus[dev];
 }
 
-template <int OUT, int W, bool M1, int FMT>
-int wgs_per_cu() {
-  read_env();
-  if (g_env_wgs) return g_env_wgs;
-  int& slot =
-      g_occ[current_device()][OUT][W == 4 ? 0 : (W == 8 ? 1 : 2)][M1 ? 1 : 0][FMT == 8 ? 1 : 0];
-  if (!slot) {
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_skinny<OUT, W, M1, FMT>, 64 * W, 0) !=
-            hipSuccess ||
-        n <= 0)
-      n = 1;
-    slot = std::min(n, kMaxWgsPerCu);
-  }
-  return slot;
-}
+// Tuning and test override of the skinny launch (qw4_tune_decode); all zero =
+// the measured policy.
+struct DecTune {
+  // 0 policy; 1 k_rows for M = 1 too (S forces the unit size, D the LDS-DMA
+  // depth 2..4); 2 k_rows with register items (S / W force unit size, waves);
+  // 3 k_dec of the given S / W / D (OUT_BF16)
+  std::atomic<int> mode{0};
+  std::atomic<int> S{0}, W{0}, D{0}, P{0};
+};
+DecTune g_dec_tune;
 
 struct Launch {
   int W, P;
-  int S;    // 0: stream-K (k_skinny); 1, 2, 4: k_rows with units of S row quads
-  bool XL;  // k_rows: activations staged in LDS
-  int DMA = 0;   // k_rows: items in LDS slots, this many per wave (0: registers)
+  int S;         // units of S row quads
+  bool XL;       // activations staged in LDS
+  int DMA = 0;   // items in LDS slots, this many per wave (0: registers)
 };
 
 // Items each k_rows wave keeps in flight (the one being computed included),
@@ -1593,37 +1200,40 @@ constexpr int rows_depth() {
 }
 
 // Workgroups per CU of k_rows without dynamic LDS (registers, waves and static
-// LDS), cached per device; the caller applies the staged activations' LDS.
+// LDS), per device; the caller applies the staged activations' LDS.
 template <int OUT, int FMT, int S, int W>
 int rows_wgs_per_cu(bool xl) {
-  static int slot[64][2] = {{0}};
-  int& v = slot[current_device()][xl ? 1 : 0];
-  if (!v) {
-    int n = 0;
+  static std::atomic<int> slot[kMaxDevices][2];
+  std::atomic<int>& v = slot[current_device()][xl ? 1 : 0];
+  int n = v.load(std::memory_order_relaxed);
+  if (!n) {
     hipError_t e = xl ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
                             &n, k_rows<OUT, FMT, S, W, true, rows_depth<OUT, FMT, S, true, W>()>, 64 * W, 0)
                       : hipOccupancyMaxActiveBlocksPerMultiprocessor(
                             &n, k_rows<OUT, FMT, S, W, false, rows_depth<OUT, FMT, S, false, W>()>, 64 * W, 0);
     if (e != hipSuccess || n <= 0) n = 1;
-    v = std::min(n, kMaxWgsPerCu);
+    n = std::min(n, 8);
+    v.store(n, std::memory_order_relaxed);
   }
-  return v;
+  return n;
 }
 
 // Static LDS of the staged-activation kernel (hipFuncGetAttributes).
 template <int OUT, int FMT, int S, int W>
 int rows_static_lds_s() {
-  static int slot[64] = {0};
-  int& v = slot[current_device()];
-  if (!v) {
+  static std::atomic<int> slot[kMaxDevices];
+  std::atomic<int>& v = slot[current_device()];
+  int n = v.load(std::memory_order_relaxed);
+  if (!n) {
     hipFuncAttributes at{};
-    v = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(
+    n = hipFuncGetAttributes(&at, reinterpret_cast<const void*>(
                                       k_rows<OUT, FMT, S, W, true, rows_depth<OUT, FMT, S, true, W>()>)) ==
                 hipSuccess
-            ? (int)at.sharedSizeBytes
-            : kLdsBytes;   // unknown: never stage
+            ? (int)at.sharedSizeBytes + 1
+            : kLdsBytes + 1;   // unknown: never stage
+    v.store(n, std::memory_order_relaxed);
   }
-  return v;
+  return n - 1;
 }
 
 template <int OUT, int FMT, int W>
@@ -1640,61 +1250,37 @@ int rows_occ(int S, bool xl) {
                   : rows_wgs_per_cu<OUT, FMT, 1, W>(xl);
 }
 
-// Default: W = 4 stream-K over every resident slot. Small outputs with short K
-// (measured on MI355X: the 19 MB qkv and 11 MB o projections) do better with
-// more waves per tile and fewer split tiles: M = 1 uses W = 16 with two
-// workgroups per tile, M > 1 W = 8 with one.
-template <int OUT, bool M1, int FMT = 4>
+// k_rows policy (measured on MI355X over the model's projections, their 8-way
+// shards and the heads): S = 1 (16-row units) when the output has fewer
+// 64-row tiles than CUs / 4 (a 896-row shard: 4.7 vs 5.6 us), S = 2 when it
+// has fewer tiles than CUs (OUT_SWIGLU pairs a gate unit with its up unit in
+// one workgroup: 32-row units keep as many workgroups as the plain GEMV's
+// 64-row units), else S = 4; M = 1: 16 waves for K >= 64 groups, else 8;
+// M > 1 and the argmax: 8 waves. Items in LDS slots (LDS-DMA):
+//  * M = 1 (the 8-bit head and the shapes k_dec does not take): 32-row
+//    units and 8 waves, 4 items per wave when the output has at least 1.5
+//    64-row tiles per CU, 3 for long K (>= 64 groups), else 2; the fused
+//    rmsnorm and the 8-bit head run faster with register items.
+//  * M > 1 (verify, heads): weight items in slots, activations loaded with
+//    each item, units of the register policy's size, 2 items per wave (3% /
+//    5% per layer at M = 9 / 16 over register items; deeper was slower).
+// Tuning override (qw4_tune_decode): mode 2 keeps register items everywhere
+// (S / W force unit size and waves), mode 1 forces the LDS-DMA depth.
+template <int OUT, int FMT>
 Launch launch_for(int out_f, int G, int M) {
-  read_env();
   const int tiles = out_f / kTileN;
-  const long long U = (long long)tiles * G;
-  const bool small = tiles < device_cus() && G <= 48 && U <= 5000;
+  const int cus = device_cus();
+  const int mode = g_dec_tune.mode.load(std::memory_order_relaxed);
+  const int tS = g_dec_tune.S.load(std::memory_order_relaxed);
+  const int tW = g_dec_tune.W.load(std::memory_order_relaxed);
+  const int tD = g_dec_tune.D.load(std::memory_order_relaxed);
+  const bool regs = mode == 2;
   Launch l;
-  l.W = small ? (M1 ? 16 : 8) : 4;
-  if (g_env_w == 4 || g_env_w == 8 || g_env_w == 16) l.W = g_env_w;
-  long long cap;
-  if (l.W == 4)
-    cap = (long long)device_cus() *
-          wgs_per_cu<OUT <= OUT_ARGMAX ? OUT : OUT_BF16, 4, M1, FMT>();   // k_skinny modes
-  else
-    cap = (long long)tiles * (l.W == 16 ? 2 : 1);
-  if (g_env_tiles_per_wg > 0) cap = std::max<long long>(1, (long long)tiles * 4 / g_env_tiles_per_wg);
-  // read on every call (tuning only)
-  const char* ep = std::getenv("QW4_SKINNY_P");
-  const int env_p = ep ? std::atoi(ep) : 0;
-  if (env_p > 0) cap = env_p;
-  // at most 64 workgroups may share a tile: keep ranges >= G / 60 blocks
-  cap = std::min(cap, std::max<long long>(1, U * 60 / G));
-  l.P = (int)std::max<long long>(1, std::min(cap, (U + l.W - 1) / l.W));
-  l.S = 0;
-  // Data-parallel k_rows (no cross-workgroup exchange) by default. Unit size
-  // and waves measured on MI355X over the model's projections, their 8-way
-  // shards and the head: S = 1 (16-row units) when the output has fewer
-  // 64-row tiles than CUs / 4 (a 896-row shard: 4.7 vs 5.6 us), S = 2
-  // (32-row units) when it has fewer tiles than CUs, else S = 4; M = 1:
-  // 16 waves for K >= 64 groups, else 8; M > 1 and the argmax: 8 waves. QW4_ROWS = 0 selects stream-K, 1 | 2 | 4 forces S (read
-  // on every call); QW4_ROWS_W forces the waves.
-  const char* er = std::getenv("QW4_ROWS");
-  const int env_rows = er ? std::atoi(er) : -1;
-  const char* ew = std::getenv("QW4_ROWS_W");
-  const int env_rows_w = ew ? std::atoi(ew) : 0;
-  l.XL = false;
-  if (env_rows == 0 && OUT <= OUT_ARGMAX) return l;   // stream-K has the basic epilogues only
-  // OUT_SWIGLU pairs a gate unit with its up unit in one workgroup: 32-row
-  // units keep as many workgroups as the plain GEMV's 64-row units
-  l.S = (env_rows == 1 || env_rows == 2 || env_rows == 4) ? env_rows
-        : (OUT != OUT_SWIGLU && 4 * tiles < device_cus()) ? 1
-        : (OUT == OUT_SWIGLU || tiles < device_cus())     ? 2
-                                                          : 4;
-  if (OUT == OUT_ARGMAX)
-    l.W = 8;   // the running argmax does not fit 16 waves' registers
-  else if (env_rows_w == 8 || env_rows_w == 16)
-    l.W = env_rows_w;
-  else if (M == 1)
-    l.W = G >= 64 ? 16 : 8;
-  else
-    l.W = 8;
+  l.S = (OUT != OUT_SWIGLU && 4 * tiles < cus) ? 1 : (OUT == OUT_SWIGLU || tiles < cus) ? 2 : 4;
+  l.W = OUT == OUT_ARGMAX ? 8 : (M == 1 && G >= 64) ? 16 : 8;
+  if ((mode == 1 || mode == 2) && (tS == 1 || tS == 2 || tS == 4) && (OUT != OUT_SWIGLU || tS != 1))
+    l.S = tS;
+  if (regs && OUT != OUT_ARGMAX && (tW == 8 || tW == 16)) l.W = tW;
   const int xbytes = M * G * kGroup * 2;
   // the kernel's static LDS + the activations within the CU's LDS
   int static_lds = 0;
@@ -1710,60 +1296,36 @@ Launch launch_for(int out_f, int G, int M) {
   else
     occ = l.W == 8 ? rows_occ<OUT, FMT, 8>(l.S, l.XL) : rows_occ<OUT, FMT, 16>(l.S, l.XL);
   if (l.XL) occ = std::max(1, std::min(occ, kLdsBytes / (static_lds + xbytes)));
-  long long pc = (long long)device_cus() * occ;
-  if (env_p > 0) pc = env_p;
   // OUT_SWIGLU: whole (gate, up) unit pairs per workgroup
-  l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? units / 2 : units, pc));
-  // M = 1: LDS-DMA items with 32-row units and 8 waves, when the slots fit
-  // the CU's LDS next to the staged activations. Measured on MI355X over the
-  // model's projections and heads: 4 items per wave when the output has at
-  // least 1.5 64-row tiles per CU (3+ units per workgroup; at 1 tile per CU,
-  // a 16384-row projection, 2 is 6% faster), 3 for long K (>= 64 groups),
-  // else 2 (deeper is slower); the 4-bit GEMV and its residual / swiglu / argmax
-  // epilogues gain up to 8%, while the fused rmsnorm and the 8-bit head run
-  // faster with register items, which stay their default. QW4_DMA = 0 keeps
-  // register items, 2 | 3 | 4 forces LDS-DMA items of that depth for every
-  // mode (read on every call); 16-row units and QW4_ROWS / QW4_ROWS_W other
-  // than 2 / 8 keep register items.
-  if (M == 1 && (env_rows == 2 || (env_rows < 0 && l.S != 1)) &&
-      (env_rows_w == 0 || env_rows_w == 8)) {
-    const char* ed = std::getenv("QW4_DMA");
-    const int dd = ed ? std::atoi(ed)
-                   : (OUT == OUT_NORM || FMT == 8) ? 0
-                   : (2 * tiles >= 3 * device_cus() ? 4 : (G >= 64 ? 3 : 2));
+  l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? units / 2 : units,
+                                             (long long)cus * occ));
+  if (regs) return l;
+  if (M == 1 && l.S != 1) {
+    const int dd = (mode == 1 && tD >= 2 && tD <= 4) ? tD
+                   : (OUT == OUT_NORM || FMT == 8)    ? 0
+                                                      : (2 * tiles >= 3 * cus ? 4 : (G >= 64 ? 3 : 2));
     const int slot = (FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256);
     const int need = xbytes + 8 * dd * slot + 2 * 8 * 2 * 16 * 16 + (OUT == OUT_NORM ? 64 : 0);
-    if (dd >= 2 && dd <= 4 && xbytes <= rows_xchunks(true) * 16 * 64 * 8 && need <= kLdsBytes) {
+    if (dd >= 2 && xbytes <= rows_xchunks(true) * 16 * 64 * 8 && need <= kLdsBytes) {
       l.DMA = dd;
       l.S = 2;
       l.W = 8;
       l.XL = true;
       const long long u2 = (long long)tiles * 2;
-      const long long pc2 = (long long)device_cus() * (kLdsBytes / need);
+      const long long pc2 = (long long)cus * (kLdsBytes / need);
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, pc2));
     }
-  } else if (M > 1 && OUT != OUT_NORM && l.S != 1 && (env_rows_w == 0 || env_rows_w == 8)) {
-    // M > 1: LDS-DMA weight items, activations loaded with each item, units
-    // of the register policy's size (64 rows when the output has at least as
-    // many tiles as CUs: each activation load then serves 4 row quads).
-    // Measured on MI355X (verify M = 9 / 16 over the model's projections): 2
-    // items per wave beat register items by 3% / 5% per layer (down M = 16:
-    // 10%); deeper is slower. QW4_DMA = 2 | 3 | 4 forces the depth, 0 keeps
-    // register items.
-    const char* ed = std::getenv("QW4_DMA");
+  } else if (M > 1 && OUT != OUT_NORM && l.S != 1) {
     const int S = l.S;
-    // (64-row units: the argmax keeps its running maxima in registers and
-    // spills past 2 items)
-    const int dd = std::min(ed ? std::atoi(ed) : 2,
-                            (OUT == OUT_ARGMAX && S == 4) ? 2 : 4);
+    const int dd = (mode == 1 && tD >= 2 && tD <= 4 && !(OUT == OUT_ARGMAX && S == 4)) ? tD : 2;
     const int slot = (FMT == 8 ? 2 * S : S) * 1024 + (FMT == 4 ? 512 : 256);
     const int need = 8 * dd * slot + 2 * 8 * S * 64 * 16;
-    if (dd >= 2 && dd <= 4 && need <= kLdsBytes) {
+    if (need <= kLdsBytes) {
       l.DMA = dd;
       l.W = 8;
       l.XL = false;
       const long long us = (long long)tiles * 4 / S;
-      const long long pc2 = (long long)device_cus() * (kLdsBytes / need);
+      const long long pc2 = (long long)cus * (kLdsBytes / need);
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? us / 2 : us, pc2));
     }
   }
@@ -1781,32 +1343,28 @@ void launch_rows_x(const SkinnyArgs& a, int S, hipStream_t st) {
     k_rows<OUT, FMT, 1, W, XL, rows_depth<OUT, FMT, 1, XL, W>()><<<a.P, 64 * W, lds, st>>>(a);
 }
 
-// Dynamic LDS above the default limit is allowed once per kernel.
-// Dynamic LDS above the default limit is allowed per kernel (one cache per
-// kernel instantiation), once per device. qw4_scratch_alloc raises every
-// LDS-DMA kernel to its maximum, so no launch -- captured into a graph or not
-// -- has to.
+// Dynamic LDS above the default limit is allowed per kernel, once per device:
+// qw4_scratch_alloc raises every LDS-DMA kernel to its maximum, so no launch --
+// captured into a graph or not -- has to. A launch that needs more than a
+// kernel was raised to (no scratch allocated on this device yet) raises it
+// under a lock.
+std::mutex g_lds_mutex;
+
 template <auto Kern>
 void allow_lds(int bytes) {
-  static int set[64] = {0};
-  int& v = set[current_device()];
-  if (bytes > v) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess)
-      v = bytes;
-    else
-      (void)hipGetLastError();   // not sticky: the launch reports what matters
-  }
+  static std::atomic<int> set[kMaxDevices];
+  std::atomic<int>& v = set[current_device()];
+  if (bytes <= v.load(std::memory_order_acquire)) return;
+  std::lock_guard<std::mutex> lock(g_lds_mutex);
+  if (bytes <= v.load(std::memory_order_relaxed)) return;
+  if (hipFuncSetAttribute(reinterpret_cast<const void*>(Kern),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, bytes) == hipSuccess)
+    v.store(bytes, std::memory_order_release);
+  else
+    (void)hipGetLastError();   // not sticky: the launch reports what matters
 }
 
 // ---- k_dec launch (M = 1, 4-bit)
-// Tuning override (qw4_tune_decode): all zero = the measured policy below.
-struct DecTune {
-  std::atomic<int> mode{0};   // 0 policy, 1 k_rows for M = 1, 3 k_dec of the given shape
-  std::atomic<int> S{0}, W{0}, D{0}, P{0};
-};
-DecTune g_dec_tune;
-
 struct DecCfg {
   int S, W, D, P;
   int lds;   // dynamic LDS bytes
@@ -1930,24 +1488,23 @@ void prepare_dma_out() {
 }
 
 void prepare_dma_lds() {
-  static bool done[64] = {false};
-  bool& d = done[current_device()];
-  if (d) return;
-  prepare_dec<OUT_BF16>();
-  prepare_dec<OUT_F32>();
-  prepare_dec<OUT_ARGMAX>();
-  prepare_dec<OUT_RES>();
-  prepare_dec<OUT_SWIGLU>();
-  prepare_dec<OUT_NORM>();
-  prepare_dma_out<OUT_BF16, 4>();
-  prepare_dma_out<OUT_F32, 4>();
-  prepare_dma_out<OUT_ARGMAX, 4>();
-  prepare_dma_out<OUT_RES, 4>();
-  prepare_dma_out<OUT_SWIGLU, 4>();
-  prepare_dma_out<OUT_NORM, 4>();
-  prepare_dma_out<OUT_BF16, 8>();
-  prepare_dma_out<OUT_ARGMAX, 8>();
-  d = true;
+  static std::once_flag once[kMaxDevices];
+  std::call_once(once[current_device()], [] {
+    prepare_dec<OUT_BF16>();
+    prepare_dec<OUT_F32>();
+    prepare_dec<OUT_ARGMAX>();
+    prepare_dec<OUT_RES>();
+    prepare_dec<OUT_SWIGLU>();
+    prepare_dec<OUT_NORM>();
+    prepare_dma_out<OUT_BF16, 4>();
+    prepare_dma_out<OUT_F32, 4>();
+    prepare_dma_out<OUT_ARGMAX, 4>();
+    prepare_dma_out<OUT_RES, 4>();
+    prepare_dma_out<OUT_SWIGLU, 4>();
+    prepare_dma_out<OUT_NORM, 4>();
+    prepare_dma_out<OUT_BF16, 8>();
+    prepare_dma_out<OUT_ARGMAX, 8>();
+  });
 }
 
 // LDS-DMA items: units of S row quads, 8 waves, D items per wave; staged
@@ -1987,20 +1544,6 @@ void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
            : launch_rows_x<OUT, FMT, 16, false>(a, l.S, st);
 }
 
-template <int OUT, bool M1, int FMT>
-void launch(const SkinnyArgs& a, int W, hipStream_t st) {
-  if (W == 16)
-    k_skinny<OUT, 16, M1, FMT><<<a.P, 1024, 0, st>>>(a);
-  else if (W == 8)
-    k_skinny<OUT, 8, M1, FMT><<<a.P, 512, 0, st>>>(a);
-  else
-    k_skinny<OUT, 4, M1, FMT><<<a.P, 256, 0, st>>>(a);
-}
-
-// Scratch regions inside qw4_scratch.partial: slots for the largest grid, then
-// the fixed-point words of every tile.
-size_t slot_floats() { return (size_t)device_cus() * kMaxWgsPerCu * 2 * 1024; }
-
 // The packed weights of either format, as the kernel sees them.
 struct WeightView {
   const void* qw;
@@ -2020,7 +1563,7 @@ struct Epi {
 template <int OUT, int FMT>
 int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scratch* s,
                void* stream, const Epi& e = Epi()) {
-  if (!y || !x || !s || !s->counters || !s->partial || !s->keys) return QW4_ERR_NULL;
+  if (!y || !x || !s || !s->counters || !s->keys) return QW4_ERR_NULL;
   if (M < 1 || M > 16) return QW4_ERR_M;
   if (((uintptr_t)x & 15) || ((uintptr_t)y & (OUT == OUT_F32 ? 15 : (OUT == OUT_BF16 ? 7 : 3))))
     return QW4_ERR_ALIGN;
@@ -2028,23 +1571,15 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   if (tiles > s->max_tiles || M > s->max_m || w.in_f > s->max_in) return QW4_ERR_SCRATCH;
   // loads address weights and x through 32-bit buffer offsets
   if (w.weight_bytes >= (1ull << 32)) return QW4_ERR_SHAPE;
-  const bool m1 = M == 1;
-  DecCfg dc{};
-  const int dmode = g_dec_tune.mode.load(std::memory_order_relaxed);
-  const bool use_dec = FMT == 4 && m1 && dmode != 1 && dec_config(w.out_f, w.G, OUT, dc);
-  const Launch l = m1 ? launch_for<OUT, true, FMT>(w.out_f, w.G, M)
-                      : launch_for<OUT, false, FMT>(w.out_f, w.G, M);
-  if ((size_t)l.P * 2 * 1024 > slot_floats() ||
-      slot_floats() + (size_t)tiles * 64 * 2 > s->partial_elems)
-    return QW4_ERR_SCRATCH;
+  if (OUT == OUT_SWIGLU && (w.out_f % (2 * kTileN))) return QW4_ERR_SHAPE;
+  if (OUT == OUT_RES && !e.res) return QW4_ERR_NULL;
+  if (OUT == OUT_NORM && !e.nw) return QW4_ERR_NULL;
   SkinnyArgs a{};
   a.qw = static_cast<const uint32_t*>(w.qw);
   a.sc = w.sc;
   a.zr = w.zr;
   a.x = x;
   a.y = y;
-  a.slots = s->partial;
-  a.sums = reinterpret_cast<uint64_t*>(s->partial + slot_floats());
   a.counters = s->counters;
   a.keys = s->keys;
   a.M = M;
@@ -2053,19 +1588,15 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.G = w.G;
   a.tiles = tiles;
   a.max_tiles = s->max_tiles;
-  a.P = l.P;
-  a.U = tiles * w.G;
-  a.slot_bytes = (uint32_t)(slot_floats() * 4);
   a.weight_bytes = (uint32_t)w.weight_bytes;
   a.res = e.res;
   a.nw = e.nw;
   a.eps = e.eps;
   a.ld = OUT == OUT_SWIGLU ? w.out_f / 2 : w.out_f;
-  if (OUT == OUT_SWIGLU && (w.out_f % (2 * kTileN))) return QW4_ERR_SHAPE;
-  if (OUT == OUT_RES && !e.res) return QW4_ERR_NULL;
-  if (OUT == OUT_NORM && (!e.nw || M > 16)) return QW4_ERR_NULL;
+  const int mode = g_dec_tune.mode.load(std::memory_order_relaxed);
   if constexpr (FMT == 4) {
-    if (use_dec) {
+    DecCfg dc{};
+    if (M == 1 && mode != 1 && mode != 2 && dec_config(w.out_f, w.G, OUT, dc)) {
       a.U = tiles * 4 / dc.S;
       a.P = dc.P;
       launch_dec<OUT>(a, dc, (hipStream_t)stream);
@@ -2073,23 +1604,13 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
       return QW4_OK;
     }
   }
+  const Launch l = launch_for<OUT, FMT>(w.out_f, w.G, M);
   if (OUT == OUT_NORM && !l.XL) return QW4_ERR_SHAPE;   // x must fit the LDS staging
-  if (l.S) {
-    a.U = tiles * 4 / l.S;
-    launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
-    QW4_LAUNCH_CHECK();
-    return QW4_OK;
-  }
-  if constexpr (OUT <= OUT_ARGMAX) {
-    if (m1)
-      launch<OUT, true, FMT>(a, l.W, (hipStream_t)stream);
-    else
-      launch<OUT, false, FMT>(a, l.W, (hipStream_t)stream);
-    QW4_LAUNCH_CHECK();
-    return QW4_OK;
-  } else {
-    return QW4_ERR_SHAPE;   // unreachable: launch_for picks k_rows for these epilogues
-  }
+  a.P = l.P;
+  a.U = tiles * 4 / l.S;
+  launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
 }
 
 template <int OUT>
@@ -2138,14 +1659,12 @@ int qw4_tune_decode(int mode, int S, int W, int D, int P) {
 }
 
 int qw4_choose_splits(int out_f, int num_groups) {
-  if (out_f < kTileN || num_groups <= 0) return 1;
-  const long long U = (long long)(out_f / kTileN) * num_groups;
-  const Launch l = launch_for<OUT_BF16, true>(out_f, num_groups, 1);
-  if (l.S) return 1;   // whole units per workgroup: no split
-  const long long P = l.P;
-  // workgroups sharing one tile, at most: ceil(G / blocks-per-workgroup) + 1
-  const long long per = std::max<long long>(1, U / P);
-  return (int)std::min<long long>(P, (num_groups + per - 1) / per + (U % P ? 1 : 0));
+  // Every skinny launch gives each workgroup whole units over all of K: no
+  // output is split across workgroups (measured on MI355X: each exchange of
+  // partials tried cost more at the tail than the imbalance it removed).
+  (void)out_f;
+  (void)num_groups;
+  return 1;
 }
 
 int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, int max_m) {
@@ -2158,8 +1677,9 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
   s->max_out = max_out;
   s->max_m = max_m;
   s->max_tiles = (max_out + kTileN - 1) / kTileN;
-  // slots (M > 1) for the largest grid, then one fixed-point word per column
-  s->partial_elems = slot_floats() + (size_t)s->max_tiles * 64 * 2;
+  // the reference's split-K capacity at splits = 1 (M rows of the widest
+  // output); no kernel here writes partials, the field is kept for callers
+  s->partial_elems = (size_t)max_m * s->max_tiles * kTileN;
   const size_t cnt_bytes = (size_t)(s->max_tiles + kKeyGroups + 1) * kCounterStride * 4;
   // argmax keys: one 128-byte line per key group
   const size_t key_bytes = (size_t)kKeyGroups * 16 * 8;
@@ -2191,10 +1711,9 @@ int qw4_scratch_free(qw4_scratch* s) {
 
 int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M) {
   if (!s) return QW4_ERR_NULL;
-  (void)splits;
+  if (splits < 1 || M < 1 || out_f < 1) return QW4_ERR_SHAPE;
   if (M > s->max_m || (out_f + kTileN - 1) / kTileN > s->max_tiles) return QW4_ERR_SCRATCH;
-  const size_t need = slot_floats() + (size_t)((out_f + kTileN - 1) / kTileN) * 64 * 2;
-  return need > s->partial_elems ? QW4_ERR_SCRATCH : QW4_OK;
+  return (size_t)splits * M * out_f > s->partial_elems ? QW4_ERR_SCRATCH : QW4_OK;
 }
 
 int qw4_gemv(uint16_t* y, const qw4_weights* w, const uint16_t* x, qw4_scratch* s,

@@ -15,7 +15,7 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.environ.get("QW4_LIB") or os.path.join(HERE, "libqwen_w4a16.so")
+LIB_PATH = os.path.join(HERE, "libqwen_w4a16.so")
 
 QW4_OK = 0
 QW4_ERR_NULL = 1
@@ -46,6 +46,7 @@ EXPORTS = (
     "qw4_w8_gemm_small", "qw4_w8_gemv_argmax",
     "qw4_rmsnorm", "qw4_residual_add", "qw4_swiglu", "qw4_gemv_residual", "qw4_gemv_swiglu",
     "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t", "qw4_mfma_peak", "qw4_tune_decode",
+    "qw4_tune_gemm", "qw4_tune_linear",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -171,6 +172,8 @@ def lib():
         "qw4_linear_max_t": ([W], i),
         "qw4_tune_decode": ([i, i, i, i, i], i),
         "qw4_mfma_peak": ([vp, i, i, vp], i),
+        "qw4_tune_gemm": ([i], i),
+        "qw4_tune_linear": ([i], i),
     }
     for name, (args, res) in sig.items():
         fn = getattr(L, name)
@@ -401,10 +404,22 @@ def linear_w4a16(y, w: W4A16Weights, x, T: int, s: GemvScratch, ws: GemmWorkspac
 
 
 def tune_decode(mode: int = 0, S: int = 0, W: int = 0, D: int = 0, P: int = 0) -> None:
-    """Tuning and test override of the M = 1 decode launch (qw4_tune_decode):
-    mode 0 = the library's policy, 1 = k_rows, 2 = k_dec; S / W / D / P force
-    unit size, waves, item depth and workgroups (0 = policy)."""
+    """Tuning and test override of the skinny launches (qw4_tune_decode): mode 0
+    the library's policy, 1 k_rows at M = 1 (D: LDS-DMA depth), 2 k_rows with
+    register items (S, W: unit size and waves), 3 k_dec of shape S / W / D;
+    P forces k_dec's workgroups (0 = policy)."""
     _chk(lib().qw4_tune_decode(mode, S, W, D, P), "tune_decode")
+
+
+def tune_gemm(schedule: int = -1) -> None:
+    """Prefill schedule override (qw4_tune_gemm): -1 cost model, 0 per tile,
+    1 stream-K, 2 hybrid."""
+    _chk(lib().qw4_tune_gemm(schedule), "tune_gemm")
+
+
+def tune_linear(max_t: int = 0) -> None:
+    """qw4_linear crossover override (qw4_tune_linear), 0 = the measured rule."""
+    _chk(lib().qw4_tune_linear(max_t), "tune_linear")
 
 
 def linear_max_t(w: W4A16Weights) -> int:

@@ -21,16 +21,14 @@ def orc():
     return oracle
 
 
-@pytest.fixture(params=["rows", "regs", "streamk"])
-def decode_path(request, monkeypatch):
+@pytest.fixture(params=["dec", "rows", "regs"])
+def decode_path(request):
     """Runs a decode/verify test through every skinny kernel form: the default
-    data-parallel k_rows (M = 1: items loaded straight into LDS), k_rows with
-    items in registers (QW4_DMA=0) and the stream-K kernel (QW4_ROWS=0); the
-    library reads both variables on every call."""
-    monkeypatch.delenv("QW4_ROWS", raising=False)
-    monkeypatch.delenv("QW4_DMA", raising=False)
-    if request.param == "streamk":
-        monkeypatch.setenv("QW4_ROWS", "0")
-    elif request.param == "regs":
-        monkeypatch.setenv("QW4_DMA", "0")
-    return request.param
+    (M = 1: the integer-MFMA k_dec; M > 1: k_rows with LDS-DMA items), k_rows
+    at M = 1 too, and k_rows with items in registers for every M, through the
+    library's tuning override (qw4_tune_decode), reset afterwards."""
+    import w4a16_hip as hip
+
+    hip.tune_decode({"dec": 0, "rows": 1, "regs": 2}[request.param])
+    yield request.param
+    hip.tune_decode(0)

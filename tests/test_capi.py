@@ -100,12 +100,10 @@ def test_python_binding_raises(hip):
 
 
 def test_choose_splits(hip):
-    # stream-K: a tile is shared by at most a handful of workgroups, never more
-    # than the whole grid, and at least one
+    # whole units per workgroup: no output is split across workgroups
     for n, g in ((248320, 40), (5120, 40), (7168, 40), (5120, 32), (5120, 136), (34816, 40),
                  (64, 4), (64, 136)):
-        s = hip.gemv_choose_splits(n, g)
-        assert 1 <= s <= max(1, (n // 64) * g // 4) + 1
+        assert hip.gemv_choose_splits(n, g) == 1
 
 
 def test_cpp_layer_exports_every_declared_function(hip):
@@ -120,14 +118,19 @@ def test_cpp_layer_exports_every_declared_function(hip):
     assert len(names) >= 20 and names <= defined, names - defined
 
 
-def test_linear_threshold_by_weight_size(hip, monkeypatch):
+def test_linear_threshold_by_weight_size(hip):
     """linear()'s skinny/prefill crossover per weight (host-only call): the
-    model's projections get 48 (gate|up), 64 (down), 96 (qkv), 112 (o_proj)."""
-    monkeypatch.delenv("QW4_LIN_MAX_T", raising=False)
+    model's projections get 48 (gate|up), 64 (down), 96 (qkv), 112 (o_proj);
+    qw4_tune_linear overrides it (the reference's QWEN_MMA_MAX_T)."""
+    hip.tune_linear(0)
     want = {(34816, 5120): 48, (5120, 17408): 64, (7168, 5120): 96, (5120, 4096): 112}
     for (n, k), t in want.items():
         w = hip.W4A16Weights()
         w.out_f, w.in_f, w.group_size, w.num_groups = n, k, 128, k // 128
         assert hip.linear_max_t(w) == t, (n, k)
-    monkeypatch.setenv("QW4_LIN_MAX_T", "33")
-    assert hip.linear_max_t(w) == 33
+    hip.tune_linear(33)
+    try:
+        assert hip.linear_max_t(w) == 33
+    finally:
+        hip.tune_linear(0)
+    assert hip.linear_max_t(w) == want[(n, k)]

@@ -1,6 +1,6 @@
-"""GPU parity of the decode kernel's LDS-DMA items (M = 1: the weight, scale and
-zero-point loads of each item go straight into LDS; QW4_DMA = items per wave,
-0 = items in registers) through the C-ABI entry points that take M = 1:
+"""GPU parity of the bf16 skinny kernel's LDS-DMA items (k_rows at M = 1: the
+weight, scale and zero-point loads of each item go straight into LDS, D items
+per wave, or into registers) through the C-ABI entry points that take M = 1:
 gemv_w4a16 / _f32, the fused residual / swiglu / rmsnorm forms, the argmax
 heads and the W8A16 GEMV (src/kernels/gemv_w4a16.cuh:88-92, :112-118,
 :147-166; src/kernels/elementwise.cuh:34-43; src/model/model.cu:697-700,
@@ -9,9 +9,10 @@ heads and the W8A16 GEMV (src/kernels/gemv_w4a16.cuh:88-92, :112-118,
 Bar: bit-exact against the register-item kernel. For the same unit size and
 waves both do the same per-unit arithmetic in the same order (only which
 workgroup owns which unit differs), so any difference is a load or wait
-error. The oracle checks of the default path (DMA at M = 1) are in
-test_gpu_parity, test_gpu_fused and test_gpu_w8; one more here per shape
-class (the GEMV bars: max-rel 1e-2, mean-abs 1e-3)."""
+error. k_rows serves M = 1 for the 8-bit head and for shapes the
+integer-MFMA decode kernel does not take; the oracle checks of every path
+are in test_gpu_parity, test_gpu_fused and test_gpu_w8; one more here per
+shape class (the GEMV bars: max-rel 1e-2, mean-abs 1e-3)."""
 import numpy as np
 import pytest
 
@@ -67,22 +68,19 @@ def _x(hip, n, sid):
     return x
 
 
-def _both(monkeypatch, run):
-    """run() with register items (32-row units, 8 waves) and with LDS-DMA items
-    at every depth; every result must equal the first."""
-    monkeypatch.setenv("QW4_DMA", "0")
-    monkeypatch.setenv("QW4_ROWS", "2")
-    monkeypatch.setenv("QW4_ROWS_W", "8")
-    want = run()
-    monkeypatch.delenv("QW4_ROWS")
-    monkeypatch.delenv("QW4_ROWS_W")
-    for depth in ("2", "3", "4", None):
-        if depth is None:
-            monkeypatch.delenv("QW4_DMA")   # the default depth
-        else:
-            monkeypatch.setenv("QW4_DMA", depth)
-        got = run()
-        assert np.array_equal(got, want), depth
+def _both(hip, run):
+    """run() with k_rows register items (32-row units, 8 waves) and with its
+    LDS-DMA items at every depth and at the policy's; every result must equal
+    the first. Set through the library's tuning override, reset afterwards."""
+    hip.tune_decode(2, S=2, W=8)
+    try:
+        want = run()
+        for depth in (2, 3, 4, 0):
+            hip.tune_decode(1, D=depth)
+            got = run()
+            assert np.array_equal(got, want), depth
+    finally:
+        hip.tune_decode(0)
 
 
 # the model's projections, one group (G < waves), an odd group count, few units
@@ -92,7 +90,7 @@ SHAPES = [(7168, 5120), (5120, 4096), (34816, 5120), (5120, 17408), (64, 128), (
 
 
 @pytest.mark.parametrize("N,K", SHAPES)
-def test_dma_gemv(hip, scratch, monkeypatch, N, K):
+def test_dma_gemv(hip, scratch, N, K):
     w, x = _gen(hip, N, K, seed=N + K), _x(hip, K, 7000 + K)
     print(f"dma gemv {N}x{K}", flush=True)
 
@@ -108,13 +106,13 @@ def test_dma_gemv(hip, scratch, monkeypatch, N, K):
         _sync()
         return host(y, np.float32)
 
-    _both(monkeypatch, bf16)
-    _both(monkeypatch, f32)
+    _both(hip, bf16)
+    _both(hip, f32)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("N,K", [(5120, 4096), (5120, 17408), (320, 640)])
-def test_dma_residual(hip, scratch, monkeypatch, N, K):
+def test_dma_residual(hip, scratch, N, K):
     w, x, h0 = _gen(hip, N, K, seed=N), _x(hip, K, 11), _x(hip, N, 12)
     print(f"dma residual {N}x{K}", flush=True)
 
@@ -124,12 +122,12 @@ def test_dma_residual(hip, scratch, monkeypatch, N, K):
         _sync()
         return host(h, np.uint16)
 
-    _both(monkeypatch, run)
+    _both(hip, run)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("N,K", [(34816, 5120), (256, 640), (4352, 5120)])
-def test_dma_swiglu(hip, scratch, monkeypatch, N, K):
+def test_dma_swiglu(hip, scratch, N, K):
     w, x = _gen(hip, N, K, seed=N + 1), _x(hip, K, 13)
     print(f"dma swiglu {N}x{K}", flush=True)
 
@@ -139,12 +137,12 @@ def test_dma_swiglu(hip, scratch, monkeypatch, N, K):
         _sync()
         return host(y, np.uint16)
 
-    _both(monkeypatch, run)
+    _both(hip, run)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("N,K", [(7168, 5120), (896, 5120), (128, 256)])
-def test_dma_rmsnorm(hip, scratch, monkeypatch, N, K):
+def test_dma_rmsnorm(hip, scratch, N, K):
     import torch
 
     w, h = _gen(hip, N, K, seed=N + 2), _x(hip, K, 14)
@@ -158,12 +156,12 @@ def test_dma_rmsnorm(hip, scratch, monkeypatch, N, K):
         _sync()
         return host(y, np.uint16)
 
-    _both(monkeypatch, run)
+    _both(hip, run)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("N", [248320, 4096, 64])
-def test_dma_argmax(hip, scratch, monkeypatch, N):
+def test_dma_argmax(hip, scratch, N):
     K = 5120
     w, x = _gen(hip, N, K, seed=N + 3), _x(hip, K, 16)
     print(f"dma argmax {N}", flush=True)
@@ -174,12 +172,12 @@ def test_dma_argmax(hip, scratch, monkeypatch, N):
         _sync()
         return host(idx, np.int32)
 
-    _both(monkeypatch, run)
+    _both(hip, run)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("N,K", [(31040, 5120), (640, 1280)])
-def test_dma_w8(hip, scratch, monkeypatch, N, K):
+def test_dma_w8(hip, scratch, N, K):
     src = _x(hip, N * K, 17)
     w = hip.quantize_w8a16(src, N, K)
     x = _x(hip, K, 18)
@@ -198,14 +196,13 @@ def test_dma_w8(hip, scratch, monkeypatch, N, K):
         _sync()
         return host(idx, np.int32)
 
-    _both(monkeypatch, bf16)
-    _both(monkeypatch, argmax)
+    _both(hip, bf16)
+    _both(hip, argmax)
     hip.w8a16_free(w)
 
 
 @pytest.mark.parametrize("N,K", [(5120, 4096), (1024, 2048), (64, 128)])
-def test_dma_vs_oracle(hip, orc, scratch, monkeypatch, N, K):
-    monkeypatch.delenv("QW4_DMA", raising=False)
+def test_dma_vs_oracle(hip, orc, scratch, N, K):
     q, zp, s = orc.gen_weights(N, K, seed=N + 1)
     x = orc.gen_x(1, K, seed=1)
     w = repack_from_logical(hip, orc, q, zp, s)
@@ -219,29 +216,25 @@ def test_dma_vs_oracle(hip, orc, scratch, monkeypatch, N, K):
 
 
 # ------------------------------------------------- M > 1 (verify, heads)
-def _both_m(monkeypatch, run, rows="2"):
+def _both_m(hip, run, rows=2):
     """M > 1: LDS-DMA weight items (activations loaded with each item) against
-    register items, 8 waves, 32-row units (rows="2") or the policy's unit size
+    register items, 8 waves, 32-row units (rows=2) or the policy's unit size
     (rows=None: 64-row units for outputs with at least as many tiles as CUs)."""
-    monkeypatch.setenv("QW4_DMA", "0")
-    if rows:
-        monkeypatch.setenv("QW4_ROWS", rows)
-    else:
-        monkeypatch.delenv("QW4_ROWS", raising=False)
-    monkeypatch.setenv("QW4_ROWS_W", "8")
-    want = run()
-    for depth in ("2", "3", "4", None):
-        if depth is None:
-            monkeypatch.delenv("QW4_DMA")   # the default for this shape
-        else:
-            monkeypatch.setenv("QW4_DMA", depth)
-        got = run()
-        assert np.array_equal(got, want), depth
+    S = rows or 0
+    hip.tune_decode(2, S=S, W=8)
+    try:
+        want = run()
+        for depth in (2, 3, 4, 0):
+            hip.tune_decode(1, S=S, D=depth)
+            got = run()
+            assert np.array_equal(got, want), depth
+    finally:
+        hip.tune_decode(0)
 
 
 @pytest.mark.parametrize("M", [2, 9, 16])
 @pytest.mark.parametrize("N,K", [(7168, 5120), (5120, 17408), (192, 384), (34816, 5120)])
-def test_dma_verify(hip, scratch, monkeypatch, N, K, M):
+def test_dma_verify(hip, scratch, N, K, M):
     w = _gen(hip, N, K, seed=N + K + M)
     x, h0 = _x(hip, M * K, 20 + M), _x(hip, M * N, 30 + M)
     print(f"dma verify M={M} {N}x{K}", flush=True)
@@ -264,10 +257,10 @@ def test_dma_verify(hip, scratch, monkeypatch, N, K, M):
         _sync()
         return host(idx, np.int32)
 
-    for rows in ("2", None):
-        _both_m(monkeypatch, gemm, rows)
-        _both_m(monkeypatch, residual, rows)
-        _both_m(monkeypatch, argmax, rows)
+    for rows in (2, None):
+        _both_m(hip, gemm, rows)
+        _both_m(hip, residual, rows)
+        _both_m(hip, argmax, rows)
     if M == 2 and N % 128 == 0:
         def swiglu():
             y = empty((M, N // 2), np.uint16)
@@ -275,12 +268,12 @@ def test_dma_verify(hip, scratch, monkeypatch, N, K, M):
             _sync()
             return host(y, np.uint16)
 
-        _both_m(monkeypatch, swiglu)
+        _both_m(hip, swiglu)
     hip.awq_free(w)
 
 
 @pytest.mark.parametrize("M", [2, 9])
-def test_dma_w8_verify(hip, scratch, monkeypatch, M):
+def test_dma_w8_verify(hip, scratch, M):
     N, K = 31040, 5120
     src = _x(hip, N * K, 19)
     w = hip.quantize_w8a16(src, N, K)
@@ -299,7 +292,7 @@ def test_dma_w8_verify(hip, scratch, monkeypatch, M):
         _sync()
         return host(idx, np.int32)
 
-    for rows in ("2", None):
-        _both_m(monkeypatch, gemm, rows)
-        _both_m(monkeypatch, argmax, rows)
+    for rows in (2, None):
+        _both_m(hip, gemm, rows)
+        _both_m(hip, argmax, rows)
     hip.w8a16_free(w)
