@@ -72,11 +72,11 @@ struct SkinnyArgs {
   const uint16_t* zr;
   const uint16_t* x;
   void* y;
-  uint32_t* counters;   // one counter per 128-byte line (kCounterStride words):
-                        //   [max_tiles, +64)      argmax arrival, per key group
-                        //   [max_tiles + 64]      argmax arrival, of key groups
+  uint32_t* counters;   // argmax arrival counters, one per 128-byte line
+                        // (kCounterStride words): [0, 64) per key group,
+                        // [64] of key groups
   uint64_t* keys;       // argmax keys [64 groups][16 rows], one line per group
-  int M, N, K, G, tiles, max_tiles, P, U;
+  int M, N, K, G, tiles, P, U;
   uint32_t weight_bytes;   // packed weights (4- or 8-bit blocks)
   const uint16_t* res;     // OUT_RES: residual [M][N] (may be y)
   const uint16_t* nw;      // OUT_NORM: rmsnorm weight [K] (applied as 1 + w)
@@ -207,8 +207,8 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
   if (lane == 0) {
     const int ngroups = a.P < kKeyGroups ? a.P : kKeyGroups;
     const uint32_t in_grp = (uint32_t)((a.P - 1 - grp) / kKeyGroups + 1);
-    uint32_t* gcnt = a.counters + (size_t)(a.max_tiles + grp) * kCounterStride;
-    uint32_t* done = a.counters + (size_t)(a.max_tiles + kKeyGroups) * kCounterStride;
+    uint32_t* gcnt = a.counters + (size_t)grp * kCounterStride;
+    uint32_t* done = a.counters + (size_t)kKeyGroups * kCounterStride;
     if (inc_dev(gcnt) == in_grp - 1 && inc_dev(done) == (uint32_t)(ngroups - 1)) {
       int32_t* idx = static_cast<int32_t*>(a.y);
       for (int m = 0; m < a.M; ++m) {
@@ -224,7 +224,7 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
         for (int m = 0; m < a.M; ++m)
           __hip_atomic_store(&a.keys[g2 * 16 + m], (uint64_t)0, __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT);
-        clear_dev(a.counters + (size_t)(a.max_tiles + g2) * kCounterStride);
+        clear_dev(a.counters + (size_t)g2 * kCounterStride);
       }
       clear_dev(done);
     }
@@ -1587,7 +1587,6 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   a.K = w.in_f;
   a.G = w.G;
   a.tiles = tiles;
-  a.max_tiles = s->max_tiles;
   a.weight_bytes = (uint32_t)w.weight_bytes;
   a.res = e.res;
   a.nw = e.nw;
@@ -1680,7 +1679,7 @@ int qw4_scratch_alloc(qw4_scratch* s, int max_in, int max_out, int min_group, in
   // the reference's split-K capacity at splits = 1 (M rows of the widest
   // output); no kernel here writes partials, the field is kept for callers
   s->partial_elems = (size_t)max_m * s->max_tiles * kTileN;
-  const size_t cnt_bytes = (size_t)(s->max_tiles + kKeyGroups + 1) * kCounterStride * 4;
+  const size_t cnt_bytes = (size_t)(kKeyGroups + 1) * kCounterStride * 4;
   // argmax keys: one 128-byte line per key group
   const size_t key_bytes = (size_t)kKeyGroups * 16 * 8;
   hipError_t e = hipMalloc((void**)&s->partial, s->partial_elems * 4);
