@@ -98,9 +98,9 @@ int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows,
  * scratch must not run concurrently.
  */
 typedef struct qw4_scratch {
-  float* partial;          /* split-K partials                               */
-  uint32_t* counters;      /* per-tile arrival counters (+1 argmax counter)  */
-  uint64_t* keys;          /* argmax keys: 64 groups x 16 rows               */
+  float* partial;          /* split-K capacity of the reference (unused here)  */
+  uint32_t* counters;      /* fused-argmax arrival counters (65 lines)       */
+  uint64_t* keys;          /* fused-argmax keys: 64 groups x 16 rows         */
   size_t partial_elems;
   int32_t max_in, max_out, max_m, max_tiles;
 } qw4_scratch;
