@@ -158,6 +158,16 @@ int qw4_gemm_mma(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
  * idx [M] int32, 1 <= M <= 16. */
 int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
                     qw4_scratch* s, void* stream);
+/* qw4_gemv_argmax without allocation. No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same results as
+ * qw4_gemv_argmax; its scratch (argmax keys and arrival counters, 16.5 KiB) is
+ * a file-scope device array the library holds per GPU until the process ends,
+ * so no scratch argument. M in 1..16 (QW4_ERR_M beyond). Calls that overlap on
+ * one GPU (several streams or threads at once) share that array and race:
+ * serialize them. Calls nothing that allocates. */
+int qw4_gemv_argmax_noalloc(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
+                            void* stream);
 
 /* ------------------------------------------------------------- prefill
  * GemmWorkspace (src/kernels/gemm_w4a16.cuh:30-35). The fused kernel needs no

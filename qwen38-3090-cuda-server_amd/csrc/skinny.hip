@@ -34,6 +34,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <climits>
 #include <atomic>
 #include <cstdlib>
 #include <cstring>
@@ -1641,6 +1642,63 @@ int run_skinny8(void* y, const qw4_w8_weights* w, const uint16_t* x, int M, qw4_
   return run_skinny<OUT, 8>(y, v, x, M, s, stream);
 }
 
+// ---- the argmax head without allocation (qw4_gemv_argmax_noalloc)
+// Its scratch: 64 key lines (16 rows of u64 keys each), then 65 arrival-counter
+// lines of 128 bytes, in the file-scope array `scratch` (16.5 KiB, one copy
+// per GPU, held until the process ends). Host code uses the array's device
+// address from hipGetSymbolAddress, never its name.
+constexpr int kNoAllocKeyWords = kKeyGroups * 16;
+constexpr int kNoAllocWords = kNoAllocKeyWords + (kKeyGroups + 1) * kCounterStride / 2;
+
+__global__ void k_zero_u64(uint64_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+}  // namespace
+}  // namespace qw4
+
+static __device__ __align__(256) uint64_t scratch[qw4::kNoAllocWords];
+
+namespace qw4 {
+namespace {
+
+// Set-up once per device (with that device current): the array's address,
+// kept per device, and one zero fill on the caller's stream (a kernel, so a
+// first call under graph capture records it; every later call relies on the
+// argmax's own reset of keys and counters at its end).
+struct NoAllocState {
+  std::once_flag once;
+  uint64_t* ptr = nullptr;
+  int status = QW4_ERR_HIP;
+};
+NoAllocState g_noalloc[kMaxDevices];
+
+int noalloc_scratch(uint64_t*& ptr, hipStream_t stream) {
+  NoAllocState& st = g_noalloc[current_device()];
+  std::call_once(st.once, [&st, stream] {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_hip_error((int)e);
+      (void)hipGetLastError();
+      return;
+    }
+    prepare_dma_lds();
+    k_zero_u64<<<(kNoAllocWords + 255) / 256, 256, 0, stream>>>(static_cast<uint64_t*>(p),
+                                                                kNoAllocWords);
+    const hipError_t e2 = hipGetLastError();
+    if (e2 != hipSuccess) {
+      set_hip_error((int)e2);
+      return;
+    }
+    st.ptr = static_cast<uint64_t*>(p);
+    st.status = QW4_OK;
+  });
+  ptr = st.ptr;
+  return st.status;
+}
+
 }  // namespace
 }  // namespace qw4
 
@@ -1738,6 +1796,22 @@ int qw4_gemm_mma(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
 int qw4_gemv_argmax(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
                     qw4_scratch* s, void* stream) {
   return run_skinny<OUT_ARGMAX>(idx, w, x, M, s, stream);
+}
+
+int qw4_gemv_argmax_noalloc(int32_t* idx, const qw4_weights* w, const uint16_t* x, int M,
+                            void* stream) {
+  if (M < 1 || M > 16) return QW4_ERR_M;   // the keys hold 16 rows
+  uint64_t* p = nullptr;
+  const int st = noalloc_scratch(p, (hipStream_t)stream);
+  if (st) return st;
+  qw4_scratch s{};
+  s.keys = p;
+  s.counters = reinterpret_cast<uint32_t*>(p + kNoAllocKeyWords);
+  s.max_m = 16;
+  s.max_in = INT32_MAX;
+  s.max_out = INT32_MAX;
+  s.max_tiles = INT32_MAX;
+  return run_skinny<OUT_ARGMAX>(idx, w, x, M, &s, stream);
 }
 
 int qw4_gemv_residual(uint16_t* h, const qw4_weights* w, const uint16_t* x, int M,

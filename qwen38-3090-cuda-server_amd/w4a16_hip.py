@@ -46,7 +46,7 @@ EXPORTS = (
     "qw4_w8_gemm_small", "qw4_w8_gemv_argmax",
     "qw4_rmsnorm", "qw4_residual_add", "qw4_swiglu", "qw4_gemv_residual", "qw4_gemv_swiglu",
     "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t", "qw4_mfma_peak", "qw4_tune_decode",
-    "qw4_tune_gemm", "qw4_tune_linear",
+    "qw4_tune_gemm", "qw4_tune_linear", "qw4_gemv_argmax_noalloc",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -173,6 +173,7 @@ def lib():
         "qw4_tune_decode": ([i, i, i, i, i], i),
         "qw4_mfma_peak": ([vp, i, i, vp], i),
         "qw4_tune_gemm": ([i], i),
+        "qw4_gemv_argmax_noalloc": ([vp, W, vp, i, vp], i),
         "qw4_tune_linear": ([i], i),
     }
     for name, (args, res) in sig.items():
@@ -340,6 +341,15 @@ def gemv_argmax_w4a16(idx, w: W4A16Weights, x, M: int, s: GemvScratch, stream=No
 
 
 # ------------------------------------------- layer steps either side
+def gemv_argmax_w4a16_noalloc(idx, w: W4A16Weights, x, M: int, stream=None) -> None:
+    """qw4_gemv_argmax_noalloc: the fused argmax head with the library's static
+    scratch (no allocation, no scratch argument; overlapping calls race)."""
+    _need(idx, M * 4, "gemv_argmax_w4a16_noalloc idx")
+    _need(x, M * w.in_f * 2, "gemv_argmax_w4a16_noalloc x")
+    _chk(lib().qw4_gemv_argmax_noalloc(_ptr(idx), C.byref(w), _ptr(x), M, _stream(stream)),
+         "gemv_argmax_w4a16_noalloc")
+
+
 def rmsnorm(out, x, w, rows: int, dim: int, eps: float, stream=None) -> None:
     """rmsnorm (elementwise.cuh:8-13): out = bf16(x * rsqrt(mean(x^2) + eps) * (1 + w))."""
     _need(out, rows * dim * 2, "rmsnorm out")
