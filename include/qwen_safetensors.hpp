@@ -9,6 +9,7 @@
 #pragma once
 #include <cstddef>
 #include <cstdint>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <unordered_map>
@@ -40,10 +41,12 @@ struct TensorView {
   }
 };
 
-// One or more files presented as a single tensor namespace.
+// One or more files presented as a single tensor namespace. The public members
+// are the reference's (safetensors.h:43-72); the open files and the tensor
+// index live behind a pointer, so this header fixes no storage layout.
 class SafeTensors {
  public:
-  SafeTensors() = default;
+  SafeTensors();
   ~SafeTensors();
   SafeTensors(const SafeTensors&) = delete;
   SafeTensors& operator=(const SafeTensors&) = delete;
@@ -54,25 +57,18 @@ class SafeTensors {
   void open_files(const std::vector<std::string>& paths);
   void close();
 
-  bool has(const std::string& name) const { return tensors_.count(name) != 0; }
+  bool has(const std::string& name) const;
   const TensorView& get(const std::string& name) const;   // throws LoaderError if absent
   const TensorView* find(const std::string& name) const;  // nullptr if absent
 
-  const std::unordered_map<std::string, TensorView>& all() const { return tensors_; }
-  size_t size() const { return tensors_.size(); }
+  const std::unordered_map<std::string, TensorView>& all() const;
+  size_t size() const;
   size_t mapped_bytes() const;
   size_t bytes_with_prefix(const std::string& prefix) const;
 
  private:
-  struct Mapping {
-    void* addr = nullptr;
-    size_t len = 0;
-    std::string path;
-  };
-  std::vector<Mapping> maps_;
-  std::unordered_map<std::string, TensorView> tensors_;
-
-  void open_one(const std::string& path);
+  struct Files;
+  std::unique_ptr<Files> files_;
 };
 
 }  // namespace qwen

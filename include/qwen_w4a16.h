@@ -247,6 +247,15 @@ int qw4_linear(uint16_t* y, const qw4_weights* w, const uint16_t* x, int T, qw4_
                qw4_workspace* ws, void* stream);
 int qw4_linear_max_t(const qw4_weights* w);
 
+/* quantize_w4a16_raw (src/model/model.cu:174-186, kernel k_quant_i4 :140-172):
+ * a bf16 [out_f][in_f] matrix (device, 16-byte aligned; the reference's
+ * lm_head ablation, --lm-head-bits 4) quantized to INT4 group-128 asymmetric
+ * (per row and group: s = (max - min) / 15, z = clamp(rint(-min / s), 0, 15),
+ * q = clamp(rint(v / s) + z, 0, 15); bf16 scale) straight into the repacked
+ * layout; allocates w like qw4_weights_alloc. */
+int qw4_quantize_w4a16(qw4_weights* w, const uint16_t* src, int out_f, int in_f, int group_size,
+                       void* stream);
+
 /* ------------------------------------------------------ 8-bit weights
  * W8A16Weights (src/kernels/gemv_w4a16.cuh:141-154), the reference's default
  * lm_head format: per (row, 128-group) a bf16 scale and int8 q in [-127, 127].

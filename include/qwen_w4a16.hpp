@@ -39,7 +39,8 @@ struct W4A16Weights {
   int out_f = 0, in_f = 0, group_size = 0, num_groups = 0;
 
   size_t qweight_bytes() const { return size_t(out_f) * in_f / 2; }
-  size_t scale_bytes() const { return size_t(out_f) * num_groups * 2; }
+  // per (64-row tile, group) one 160-byte record: 64 bf16 scales + 16 zero words
+  size_t scale_bytes() const { return size_t(out_f) / 64 * num_groups * 160; }
   size_t zp_bytes() const { return size_t(out_f) * num_groups / 2; }
   size_t total_bytes() const { return qweight_bytes() + scale_bytes() + zp_bytes(); }
 };
@@ -99,6 +100,10 @@ struct W8A16Weights {
 
 void quantize_w8a16(W8A16Weights& dst, const __hip_bfloat16* src, int out_f, int in_f,
                     int group_size, hipStream_t stream = 0);
+// quantize_w4a16_raw (src/model/model.cu:174-186): the INT4 g128 lm_head
+// quantizer, straight into the repacked layout (no host sync).
+void quantize_w4a16_raw(W4A16Weights& dst, const __hip_bfloat16* src, int rows, int cols,
+                        int group, hipStream_t stream = 0);
 void gemv_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,
                 GemvScratch& s, hipStream_t stream = 0);
 void gemm_small_w8a16(__hip_bfloat16* y, const W8A16Weights& w, const __hip_bfloat16* x,

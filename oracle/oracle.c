@@ -332,6 +332,45 @@ void or_w8_quantize(const uint16_t* w, int N, int K, int group, int8_t* q, uint1
     }
 }
 
+/* The reference's INT4 g128 lm_head quantizer, k_quant_i4
+ * (src/model/model.cu:140-172), over a bf16 [N][K] matrix, writing the
+ * compressed-tensors (A0) tensors awq_repack takes (model.cu:176-183):
+ * packed [N][K/8] (element e of a word at bits 4e), bf16 scale [N][G],
+ * zero points [N/8][G] (row r at bits 4 (r % 8) of word (r / 8, g)), all
+ * nibbles 0..15 (w = (q - z) s). fp32 arithmetic as the reference's CUDA:
+ * IEEE division, rintf (round half even) for __float2int_rn. */
+void or_quant_i4(const uint16_t* w, int N, int K, int group, uint32_t* packed, uint16_t* scale,
+                 uint32_t* zp) {
+  const int G = K / group;
+  memset(zp, 0, (size_t)(N / 8) * G * 4);
+  for (int r = 0; r < N; ++r)
+    for (int g = 0; g < G; ++g) {
+      const uint16_t* src = w + (size_t)r * K + (size_t)g * group;
+      float lo = 1e30f, hi = -1e30f;
+      for (int i = 0; i < group; ++i) {
+        const float v = or_bf16_to_f32(src[i]);
+        lo = fminf(lo, v);
+        hi = fmaxf(hi, v);
+      }
+      float s = (hi - lo) / 15.0f;
+      if (!(s > 0.f)) s = 1e-8f;
+      int z = (int)rintf(-lo / s);
+      z = z < 0 ? 0 : (z > 15 ? 15 : z);
+      scale[(size_t)r * G + g] = or_f32_to_bf16(s);
+      zp[(size_t)(r >> 3) * G + g] |= (uint32_t)z << ((r & 7) * 4);
+      const float inv = 1.0f / s;
+      for (int i = 0; i < group; i += 8) {
+        uint32_t word = 0;
+        for (int k = 0; k < 8; ++k) {
+          int q = (int)rintf(or_bf16_to_f32(src[i + k]) * inv) + z;
+          q = q < 0 ? 0 : (q > 15 ? 15 : q);
+          word |= (uint32_t)q << (4 * k);
+        }
+        packed[(size_t)r * (K / 8) + ((size_t)g * group + i) / 8] = word;
+      }
+    }
+}
+
 typedef struct {
   const uint16_t* x;
   int M;

@@ -106,6 +106,9 @@ int or_cpu_w4a16_matmul(const uint16_t* x, int M, const uint32_t* packed,
  * inv = mx > 0 ? 127 / mx : 0 (fp32, from mx, not from the rounded s),
  * q = clamp(rint(w * inv), -127, 127). Dequantized weight: q * float(s). */
 void or_w8_quantize(const uint16_t* w, int N, int K, int group, int8_t* q, uint16_t* s);
+/* k_quant_i4 (src/model/model.cu:140-172): INT4 g128 asymmetric, A0 tensors. */
+void or_quant_i4(const uint16_t* w, int N, int K, int group, uint32_t* packed, uint16_t* scale,
+                 uint32_t* zp);
 /* y[m][n] = sum_k x[m][k] * q[n][k] * s[n][k / group], fp64 (k_gemv8,
  * src/kernels/gemv_w4a16.cu:498-523, with fp64 accumulation). */
 void or_w8_matmul_f64(const uint16_t* x, int M, const int8_t* q, const uint16_t* s, int N,

@@ -73,6 +73,7 @@ def lib():
     L.or_argmax_rows_f32.argtypes = [_f32p, i, i, _i32p]
     L.or_argmax_rows_bf16.argtypes = [_u16p, i, i, _i32p]
     L.or_w8_quantize.argtypes = [_u16p, i, i, i, _i8p, _u16p]
+    L.or_quant_i4.argtypes = [_u16p, i, i, i, _u32p, _u16p, _u32p]
     L.or_w8_matmul_f64.argtypes = [_u16p, i, _i8p, _u16p, i, i, i, _f64p, i]
     L.or_f32_to_bf16.argtypes = [C.c_float]
     L.or_f32_to_bf16.restype = C.c_uint16
@@ -241,6 +242,20 @@ def matmul_f64(x, q, zp, s, group=128, round_w=False, threads=None):
     fn(x, M, _c(q, np.uint8), _c(zp, np.uint8), _c(s, np.uint16), N, K, group, y,
        threads or nthreads())
     return y
+
+
+def quant_i4(w_bf16, group=128):
+    """INT4 g128 asymmetric quantizer (k_quant_i4, src/model/model.cu:140-172):
+    bf16 [N][K] -> compressed-tensors tensors (packed u32 [N][K/8], scale bf16
+    bits [N][G], zero points u32 [N/8][G]; nibbles 0..15)."""
+    w = _c(w_bf16, np.uint16)
+    N, K = w.shape
+    G = K // group
+    packed = np.empty((N, K // 8), np.uint32)
+    scale = np.empty((N, G), np.uint16)
+    zp = np.empty((N // 8, G), np.uint32)
+    lib().or_quant_i4(w, N, K, group, packed, scale, zp)
+    return packed, scale, zp
 
 
 def w8_quantize(w_bf16, group=128):

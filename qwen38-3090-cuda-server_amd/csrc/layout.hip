@@ -113,6 +113,52 @@ __global__ void k_dequant_rows(uint16_t* __restrict__ dst, const uint32_t* __res
   *reinterpret_cast<u32x4*>(dst + (size_t)r * K + 8 * wi) = u32x4{o[0], o[1], o[2], o[3]};
 }
 
+// ------------------------------------------------------- INT4 quantizer
+// The reference's k_quant_i4 (src/model/model.cu:140-172), the INT4 g128
+// asymmetric lm_head quantizer, writing the repacked layout directly: one
+// thread per (tile, group, row quad c); for each of its 4 rows and the group:
+// lo / hi = min / max (fp32 of the bf16 values), s = (hi - lo) / 15 (1e-8 if
+// not > 0), z = clamp(rint(-lo / s), 0, 15), stored scale bf16(s); each value
+// q = clamp(rint(v * (1 / s)) + z, 0, 15) with the unrounded fp32 s. IEEE
+// division and round-half-even as the reference's CUDA arithmetic.
+__global__ void k_quant_i4(uint32_t* __restrict__ qw, uint16_t* __restrict__ sc,
+                           uint16_t* __restrict__ zr, const uint16_t* __restrict__ src, int N,
+                           int K, int G) {
+  const long long t = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= (long long)(N / 4) * G) return;
+  const int g = (int)(t % G), quad = (int)(t / G);
+  const int b = quad >> 4, c = quad & 15;
+  const size_t blk = (size_t)b * G + g;
+  uint32_t zbits = 0;
+  for (int i = 0; i < 4; ++i) {
+    const int rr = 4 * c + i, n = b * kTileN + rr;
+    const uint16_t* row = src + (size_t)n * K + (size_t)g * kGroup;
+    float lo = 1e30f, hi = -1e30f;
+    for (int e = 0; e < kGroup; ++e) {
+      const float v = bf16_bits_to_f32(row[e]);
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+    }
+    float s = (hi - lo) / 15.0f;
+    if (!(s > 0.f)) s = 1e-8f;
+    const int z = max(0, min(15, __float2int_rn(-lo / s)));
+    sc[blk * kMetaU16 + rr] = to_bf16(s);
+    zbits |= (uint32_t)z << (4 * i);
+    const float inv = 1.0f / s;
+    const int p = tile_pos_of_row(rr);
+    for (int k8 = 0; k8 < kGroup / 8; ++k8) {   // word w of chunk j: k = 32 j + 8 w + e
+      uint32_t word = 0;
+      for (int e = 0; e < 8; ++e) {
+        const int q = max(0, min(15, __float2int_rn(bf16_bits_to_f32(row[8 * k8 + e]) * inv) + z));
+        word |= (uint32_t)q << (4 * slot_of_elem(e));
+      }
+      qw[blk * kWordsPerBlock + (k8 >> 2) * 256 + p * 4 + (k8 & 3)] = word;
+    }
+  }
+  zr[blk * 16 + c] = (uint16_t)zbits;
+  sc[blk * kMetaU16 + 64 + c] = (uint16_t)zbits;
+}
+
 // ------------------------------------------------------------ 8-bit weights
 // W8A16 quantizer, the reference's k_quant_w8 (src/kernels/gemv_w4a16.cu:478-495)
 // writing the 8-bit block layout directly: one thread per (row n, group g);
@@ -468,6 +514,21 @@ int qw4_dequant_rows(uint16_t* dst, const qw4_weights* w, int row0, int nrows, v
   const size_t n = (size_t)nrows * (w->in_f / 8);
   k_dequant_rows<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(
       dst, w->qweight, w->scale, w->zeros, row0, nrows, w->in_f, w->num_groups);
+  QW4_LAUNCH_CHECK();
+  return QW4_OK;
+}
+
+int qw4_quantize_w4a16(qw4_weights* w, const uint16_t* src, int out_f, int in_f, int group_size,
+                       void* stream) {
+  if (!w || !src) return QW4_ERR_NULL;
+  std::memset(w, 0, sizeof(*w));
+  if (group_size != kGroup) return QW4_ERR_GROUP;
+  if (out_f <= 0 || out_f % kTileN || in_f <= 0 || in_f % kGroup) return QW4_ERR_SHAPE;
+  const int st = qw4_weights_alloc(w, out_f, in_f, group_size, stream);
+  if (st) return st;
+  const size_t n = (size_t)(out_f / 4) * w->num_groups;
+  k_quant_i4<<<blocks_for(n, 256), 256, 0, (hipStream_t)stream>>>(w->qweight, w->scale, w->zeros,
+                                                                  src, out_f, in_f, w->num_groups);
   QW4_LAUNCH_CHECK();
   return QW4_OK;
 }

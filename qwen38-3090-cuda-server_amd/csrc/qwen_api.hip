@@ -157,6 +157,13 @@ void gemv_argmax_w4a16(int32_t* idx, const W4A16Weights& w, const __hip_bfloat16
   check(qw4_gemv_argmax(idx, &v, u16(x), M, &s.impl, stream), "gemv_argmax_w4a16");
 }
 
+void quantize_w4a16_raw(W4A16Weights& dst, const __hip_bfloat16* src, int rows, int cols,
+                        int group, hipStream_t stream) {
+  qw4_weights v{};
+  check(qw4_quantize_w4a16(&v, u16(src), rows, cols, group, stream), "quantize_w4a16_raw");
+  adopt(dst, v);
+}
+
 void quantize_w8a16(W8A16Weights& dst, const __hip_bfloat16* src, int out_f, int in_f,
                     int group_size, hipStream_t stream) {
   qw4_w8_weights v{};

@@ -274,34 +274,48 @@ bool ends_with(const std::string& s, const char* suf) {
 
 }  // namespace
 
+// The open files (read-only mappings) and the index of every tensor in them.
+struct SafeTensors::Files {
+  struct Region {
+    const uint8_t* base = nullptr;
+    size_t bytes = 0;
+  };
+  std::vector<Region> regions;
+  std::unordered_map<std::string, TensorView> index;
+
+  void add_file(const std::string& path);
+  void release() {
+    for (const Region& r : regions)
+      if (r.base) munmap(const_cast<uint8_t*>(r.base), r.bytes);
+    regions.clear();
+    index.clear();
+  }
+};
+
+SafeTensors::SafeTensors() : files_(new Files) {}
 SafeTensors::~SafeTensors() { close(); }
 
-void SafeTensors::close() {
-  for (auto& m : maps_)
-    if (m.addr) munmap(m.addr, m.len);
-  maps_.clear();
-  tensors_.clear();
-}
+void SafeTensors::close() { files_->release(); }
 
 void SafeTensors::open_files(const std::vector<std::string>& paths) {
-  for (const auto& p : paths) open_one(p);
+  for (const auto& p : paths) files_->add_file(p);
 }
 
 void SafeTensors::open_dir(const std::string& dir) {
   DIR* d = opendir(dir.c_str());
   if (!d) throw LoaderError(dir + ": cannot open directory");
-  std::vector<std::string> files;
+  std::vector<std::string> found;
   while (dirent* ent = readdir(d)) {
     const std::string name = ent->d_name;
-    if (ends_with(name, ".safetensors")) files.push_back(dir + "/" + name);
+    if (ends_with(name, ".safetensors")) found.push_back(dir + "/" + name);
   }
   closedir(d);
-  if (files.empty()) throw LoaderError(dir + ": no *.safetensors files");
-  std::sort(files.begin(), files.end());
-  open_files(files);
+  if (found.empty()) throw LoaderError(dir + ": no *.safetensors files");
+  std::sort(found.begin(), found.end());
+  open_files(found);
 }
 
-void SafeTensors::open_one(const std::string& path) {
+void SafeTensors::Files::add_file(const std::string& path) {
   const int fd = ::open(path.c_str(), O_RDONLY);
   if (fd < 0) throw LoaderError(path + ": cannot open");
   struct stat st;
@@ -313,10 +327,9 @@ void SafeTensors::open_one(const std::string& path) {
   void* addr = mmap(nullptr, len, PROT_READ, MAP_PRIVATE, fd, 0);
   ::close(fd);
   if (addr == MAP_FAILED) throw LoaderError(path + ": mmap failed");
-  maps_.push_back({addr, len, path});
-  const int shard = (int)maps_.size() - 1;
   const uint8_t* base = static_cast<const uint8_t*>(addr);
-
+  regions.push_back({base, len});
+  const int shard = (int)regions.size() - 1;
   uint64_t hlen = 0;
   for (int k = 0; k < 8; ++k) hlen |= (uint64_t)base[k] << (8 * k);
   if (hlen > len - 8 || hlen > (100ull << 20))
@@ -356,31 +369,39 @@ void SafeTensors::open_one(const std::string& path) {
       throw LoaderError(path + ": tensor '" + kv.first + "' size does not match its shape");
     v.data = base + data0 + (size_t)b.i;
     v.shard = shard;
-    if (!tensors_.emplace(kv.first, std::move(v)).second)
+    if (!index.emplace(kv.first, std::move(v)).second)
       throw LoaderError(path + ": tensor '" + kv.first + "' appears twice");
   }
 }
 
+bool SafeTensors::has(const std::string& name) const { return files_->index.count(name) != 0; }
+
+const std::unordered_map<std::string, TensorView>& SafeTensors::all() const {
+  return files_->index;
+}
+
+size_t SafeTensors::size() const { return files_->index.size(); }
+
 const TensorView& SafeTensors::get(const std::string& name) const {
-  auto it = tensors_.find(name);
-  if (it == tensors_.end()) throw LoaderError("tensor not found: " + name);
-  return it->second;
+  const TensorView* v = find(name);
+  if (!v) throw LoaderError("tensor not found: " + name);
+  return *v;
 }
 
 const TensorView* SafeTensors::find(const std::string& name) const {
-  auto it = tensors_.find(name);
-  return it == tensors_.end() ? nullptr : &it->second;
+  auto it = files_->index.find(name);
+  return it == files_->index.end() ? nullptr : &it->second;
 }
 
 size_t SafeTensors::mapped_bytes() const {
   size_t n = 0;
-  for (const auto& m : maps_) n += m.len;
+  for (const auto& r : files_->regions) n += r.bytes;
   return n;
 }
 
 size_t SafeTensors::bytes_with_prefix(const std::string& prefix) const {
   size_t n = 0;
-  for (const auto& kv : tensors_)
+  for (const auto& kv : files_->index)
     if (kv.first.compare(0, prefix.size(), prefix) == 0) n += kv.second.nbytes;
   return n;
 }

@@ -47,6 +47,7 @@ EXPORTS = (
     "qw4_rmsnorm", "qw4_residual_add", "qw4_swiglu", "qw4_gemv_residual", "qw4_gemv_swiglu",
     "qw4_gemv_rmsnorm", "qw4_linear", "qw4_linear_max_t", "qw4_mfma_peak", "qw4_tune_decode",
     "qw4_tune_gemm", "qw4_tune_linear", "qw4_gemv_argmax_noalloc",
+    "qw4_quantize_w4a16",
 )
 
 # safetensors dtype order (qw4_st_tensor.dtype)
@@ -174,6 +175,7 @@ def lib():
         "qw4_mfma_peak": ([vp, i, i, vp], i),
         "qw4_tune_gemm": ([i], i),
         "qw4_gemv_argmax_noalloc": ([vp, W, vp, i, vp], i),
+        "qw4_quantize_w4a16": ([W, vp, i, i, i, vp], i),
         "qw4_tune_linear": ([i], i),
     }
     for name, (args, res) in sig.items():
@@ -438,6 +440,16 @@ def linear_max_t(w: W4A16Weights) -> int:
 
 
 # ------------------------------------------------------- 8-bit lm_head
+def quantize_w4a16_raw(src, rows: int, cols: int, group: int = 128, stream=None) -> W4A16Weights:
+    """quantize_w4a16_raw (src/model/model.cu:174-186): bf16 [rows][cols] -> INT4
+    g128 asymmetric, repacked (the reference's INT4 lm_head)."""
+    _need(src, rows * cols * 2, "quantize_w4a16_raw src")
+    w = W4A16Weights()
+    _chk(lib().qw4_quantize_w4a16(C.byref(w), _ptr(src), rows, cols, group, _stream(stream)),
+         "quantize_w4a16_raw")
+    return w
+
+
 def quantize_w8a16(src, out_f: int, in_f: int, group_size: int = 128, stream=None) -> W8A16Weights:
     """quantize_w8a16 (gemv_w4a16.cuh:156-157): bf16 [out_f][in_f] -> 8-bit weights."""
     _need(src, out_f * in_f * 2, "quantize_w8a16 src")

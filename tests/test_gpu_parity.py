@@ -179,6 +179,23 @@ def test_verify_skinny(hip, orc, scratch, decode_path, M, N, K):
     hip.awq_free(w)
 
 
+@pytest.mark.parametrize("N,K", [(5120, 5120), (5120, 4096), (34816, 5120)])
+def test_verify_config3_shapes(hip, orc, scratch, N, K):
+    """BASELINE config 3 at the config-1 shape (5120x5120) and at o_proj and
+    gate|up, M in {9, 12, 16}, against the oracle (one weight set per shape)."""
+    import torch
+
+    q, zp, s = orc.gen_weights(N, K, seed=N + 31 * K)
+    w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
+    for M in (9, 12, 16):
+        x = orc.gen_x(M, K, seed=M + N)
+        y = empty((M, N), np.uint16)
+        hip.gemm_small_w4a16(y, w, dev(x), M, scratch)
+        torch.cuda.synchronize()
+        _check_bf16(orc, host(y, np.uint16), orc.matmul_f64(x, q, zp, s), f"config3 M={M} {N}x{K}")
+    hip.awq_free(w)
+
+
 def test_mma_entry_matches_small(hip, orc, scratch):
     import torch
 
@@ -246,7 +263,9 @@ def gemm_ws(hip):
                                    (512, 5120, 17408), (200, 5184, 1536), (777, 5184, 4096),
                                    (300, 5120, 2176), (64, 896, 640),
                                    # 340 tiles: 256 whole, 84 split over the CUs
-                                   (1100, 17408, 5120)])
+                                   (1100, 17408, 5120),
+                                   # config 4 down at M=1024: stream-K, the most cut tiles
+                                   (1024, 5120, 17408)])
 @pytest.mark.parametrize("use_ws", [False, True])
 def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     """BASELINE config 4 semantics: RNE(bf16) dequant, fp32 accumulation, bf16 out.
@@ -276,7 +295,8 @@ def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     hip.awq_free(w)
 
 
-@pytest.mark.parametrize("M,N,K", [(4096, 17408, 5120), (4096, 5120, 17408), (1024, 17408, 5120)])
+@pytest.mark.parametrize("M,N,K", [(4096, 17408, 5120), (4096, 5120, 17408), (1024, 17408, 5120),
+                                   (1024, 5120, 17408)])
 def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
     """Full-size prefill against a torch fp32 GEMM of the bit-exact dequantized
     weights (dequant_rows is pinned bit-exact above)."""

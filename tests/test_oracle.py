@@ -310,3 +310,85 @@ def test_w8_matmul_closed_forms(orc):
     xr = orc.f32_to_bf16(rng.standard_normal((3, K)).astype(np.float32))
     ref = orc.bf16_to_f32(xr).astype(np.float64) @ (q * sf).T
     assert np.allclose(orc.w8_matmul_f64(xr, q, s), ref, rtol=1e-12, atol=1e-12)
+
+
+# ------------------------------------------------------------ INT4 quantizer
+def _i4_unpack(orc, packed, scale, zp, N, K):
+    q, z, s = orc.unpack_ct(packed, scale, zp, N, K)
+    return q.astype(int), z.astype(int), orc.bf16_to_f32(s)
+
+
+def test_quant_i4_recovers_even_grids(orc):
+    """Groups of 16 evenly spaced values (i - z0) d, d a power of two, all 16
+    present: s = 15 d / 15 = d exactly, z = z0, q = i, and the dequantized
+    (q - z) s is the source exactly (k_quant_i4, model.cu:140-172)."""
+    rng = np.random.default_rng(3)
+    N, K = 16, 512
+    G = K // 128
+    z0 = rng.integers(0, 16, (N, G))
+    d = 2.0 ** rng.integers(-10, 0, (N, G))
+    idx = rng.integers(0, 16, (N, K))
+    for g in range(G):
+        idx[:, g * 128:g * 128 + 16] = np.arange(16)   # every level present
+    w = (idx - np.repeat(z0, 128, axis=1)) * np.repeat(d, 128, axis=1)
+    packed, scale, zp = orc.quant_i4(orc.f32_to_bf16(w.astype(np.float32)))
+    q, z, s = _i4_unpack(orc, packed, scale, zp, N, K)
+    assert np.array_equal(q, idx)
+    assert np.array_equal(z, z0)
+    assert np.array_equal(s, d.astype(np.float32))
+    assert np.array_equal((q - np.repeat(z, 128, axis=1)) * np.repeat(s, 128, axis=1), w)
+
+
+def test_quant_i4_constant_groups(orc):
+    """max == min: s = 1e-8 (stored bf16(1e-8)); a positive constant gives z = 0
+    and q = 15 (both clamped), a negative one z = 15 and q = 0, zero z = q = 0."""
+    N, K = 8, 384
+    w = np.zeros((N, K), np.float32)
+    w[:, :128], w[:, 128:256] = 0.75, -2.5
+    packed, scale, zp = orc.quant_i4(orc.f32_to_bf16(w))
+    q, z, s = _i4_unpack(orc, packed, scale, zp, N, K)
+    assert np.all(s == orc.bf16_to_f32(orc.f32_to_bf16(np.float32(1e-8))))
+    assert np.all(z[:, 0] == 0) and np.all(q[:, :128] == 15)
+    assert np.all(z[:, 1] == 15) and np.all(q[:, 128:256] == 0)
+    assert np.all(z[:, 2] == 0) and np.all(q[:, 256:] == 0)
+
+
+def test_quant_i4_rounds_half_to_even(orc):
+    """lo = 0, hi = 15 d with d a power of two: s = d, 1/s exact, so the values
+    (j + 1/2) d sit exactly on halves and rint sends them to the even
+    neighbour (the reference's __float2int_rn)."""
+    d = 2.0 ** -5
+    row = np.zeros(128, np.float32)
+    row[1] = 15 * d
+    halves = np.arange(0, 14) + 0.5
+    row[2:2 + halves.size] = halves * d
+    packed, scale, zp = orc.quant_i4(orc.f32_to_bf16(np.tile(row, (8, 1))))
+    q, z, s = _i4_unpack(orc, packed, scale, zp, 8, 128)
+    assert s[0, 0] == d and z[0, 0] == 0 and q[0, 1] == 15
+    want = np.rint(halves).astype(int)
+    assert np.array_equal(q[0, 2:2 + halves.size], want) and all(v % 2 == 0 for v in want)
+
+
+def test_quant_i4_brute_force_and_error_bound(orc):
+    """Random bf16 rows against an independent float32 numpy restatement of
+    the same steps (min / max, IEEE division, rint), and the reconstruction
+    error within one step of the unrounded scale plus the scale's bf16
+    rounding over 15 steps."""
+    rng = np.random.default_rng(4)
+    N, K = 24, 640
+    w = orc.f32_to_bf16((rng.standard_normal((N, K)) * 0.03).astype(np.float32))
+    packed, scale, zp = orc.quant_i4(w)
+    q, z, s = _i4_unpack(orc, packed, scale, zp, N, K)
+    f = orc.bf16_to_f32(w).reshape(N, K // 128, 128)
+    lo, hi = f.min(axis=2), f.max(axis=2)
+    sf = (hi - lo) / np.float32(15)
+    sf = np.where(sf > 0, sf, np.float32(1e-8)).astype(np.float32)
+    zf = np.clip(np.rint(-lo / sf), 0, 15).astype(int)
+    inv = (np.float32(1) / sf).astype(np.float32)
+    qf = np.clip(np.rint(f * inv[..., None]).astype(int) + zf[..., None], 0, 15)
+    assert np.array_equal(z, zf)
+    assert np.array_equal(q, qf.reshape(N, K))
+    assert np.array_equal(orc.f32_to_bf16(sf), orc.f32_to_bf16(s))
+    rec = (q.reshape(N, K // 128, 128) - z[..., None]) * s[..., None]
+    bound = sf[..., None] * 1.0 + 15 * np.abs(s - sf)[..., None] + 1e-12
+    assert np.all(np.abs(rec - f) <= bound)
