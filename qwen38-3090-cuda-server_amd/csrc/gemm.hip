@@ -456,6 +456,7 @@ int device_cus() {
 // Tuning and test override of the prefill schedule (qw4_tune_gemm): -1 the
 // cost model, 0 per tile, 1 stream-K, 2 hybrid.
 std::atomic<int> g_gemm_schedule{-1};
+std::atomic<int> g_gemm_nh{1};   // weight rows per wave: 1 = 32-row halves, 2 = 64-row tiles
 
 }  // namespace
 }  // namespace qw4
@@ -486,9 +487,10 @@ int qw4_workspace_free(qw4_workspace* ws) {
   return QW4_OK;
 }
 
-int qw4_tune_gemm(int schedule) {
-  if (schedule < -1 || schedule > 2) return QW4_ERR_SHAPE;
+int qw4_tune_gemm(int schedule, int variant) {
+  if (schedule < -1 || schedule > 2 || variant < 0 || variant > 2) return QW4_ERR_SHAPE;
   g_gemm_schedule.store(schedule, std::memory_order_relaxed);
+  g_gemm_nh.store(variant == 2 ? 2 : 1, std::memory_order_relaxed);
   return QW4_OK;
 }
 
@@ -550,11 +552,18 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
       grid = cus;
     }
     hipStream_t s = (hipStream_t)stream;
-    k_gemm<1><<<grid, 512, 0, s>>>(a);
+    const int nh = g_gemm_nh.load(std::memory_order_relaxed);
+    if (nh == 2)
+      k_gemm<2><<<grid, 512, 0, s>>>(a);
+    else
+      k_gemm<1><<<grid, 512, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
     if (a.full != nt) {   // the split tiles
       const int fb = (nt - a.full) * G2_WAVES * kFixParts;
-      k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
+      if (nh == 2)
+        k_gemm_fixup<2><<<fb, 64, 0, s>>>(a);
+      else
+        k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;

@@ -173,7 +173,7 @@ def lib():
         "qw4_linear_max_t": ([W], i),
         "qw4_tune_decode": ([i, i, i, i, i], i),
         "qw4_mfma_peak": ([vp, i, i, vp], i),
-        "qw4_tune_gemm": ([i], i),
+        "qw4_tune_gemm": ([i, i], i),
         "qw4_gemv_argmax_noalloc": ([vp, W, vp, i, vp], i),
         "qw4_quantize_w4a16": ([W, vp, i, i, i, vp], i),
         "qw4_tune_linear": ([i], i),
@@ -423,10 +423,10 @@ def tune_decode(mode: int = 0, S: int = 0, W: int = 0, D: int = 0, P: int = 0) -
     _chk(lib().qw4_tune_decode(mode, S, W, D, P), "tune_decode")
 
 
-def tune_gemm(schedule: int = -1) -> None:
-    """Prefill schedule override (qw4_tune_gemm): -1 cost model, 0 per tile,
-    1 stream-K, 2 hybrid."""
-    _chk(lib().qw4_tune_gemm(schedule), "tune_gemm")
+def tune_gemm(schedule: int = -1, variant: int = 0) -> None:
+    """Prefill override (qw4_tune_gemm): schedule -1 cost model, 0 per tile,
+    1 stream-K, 2 hybrid; variant 0 default, 2 whole 64-row tiles per wave."""
+    _chk(lib().qw4_tune_gemm(schedule, variant), "tune_gemm")
 
 
 def tune_linear(max_t: int = 0) -> None:
