@@ -105,20 +105,24 @@ __device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const G2Rsr
   }
 }
 
-// Issue this wave's share of the activation rows of group g into buf. `act`
-// covers rows [m0, M) of A; rows past M lie outside it and read as zeros.
-// voff[i % 4] is the lane's byte offset of instruction i relative to its
-// first row (the swizzle repeats every 4 instructions).
+// Issue load i (of G2_ROWBLOCKS / G2_WAVES) of this wave's share of the
+// activation rows of group g into buf. `act` covers rows [m0, M); rows past M
+// lie outside it and read as zeros. voff[i % 4] is the lane's byte offset of
+// load i relative to its first row (the swizzle repeats every 4 loads).
+constexpr int G2_ACT_LOADS = G2_ROWBLOCKS / G2_WAVES;   // per wave and group: 8
+static_assert(G2_ACT_LOADS == 8, "two activation loads in each of k-steps 0-3 of a group");
+__device__ __forceinline__ void g2_load_act1(__amdgpu_buffer_rsrc_t act, const uint32_t (&voff)[4],
+                                             uint32_t row_bytes, u32x4* buf, int g, int wave,
+                                             int i) {
+  const int rb = wave * G2_ACT_LOADS + i;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(act, buf + rb * 64, 16,
+                                           voff[i & 3] + (uint32_t)(4 * rb) * row_bytes,
+                                           (uint32_t)g * (kGroup * 2), 0, 0);
+}
 __device__ __forceinline__ void g2_load_act(__amdgpu_buffer_rsrc_t act, const uint32_t (&voff)[4],
                                             uint32_t row_bytes, u32x4* buf, int g, int wave) {
-  constexpr int per_wave = G2_ROWBLOCKS / G2_WAVES;
 #pragma unroll
-  for (int i = 0; i < per_wave; ++i) {
-    const int rb = wave * per_wave + i;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(act, buf + rb * 64, 16,
-                                             voff[i & 3] + (uint32_t)(4 * rb) * row_bytes,
-                                             (uint32_t)g * (kGroup * 2), 0, 0);
-  }
+  for (int i = 0; i < G2_ACT_LOADS; ++i) g2_load_act1(act, voff, row_bytes, buf, g, wave, i);
 }
 
 // One packed word -> 8 bf16 weights RNE((q - z) s), c = -z s, in the order
@@ -203,10 +207,13 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
     __syncthreads();
     const int sb = (g - g0) & 1;
     const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
-    if (g + 1 < g1) {
-      g2_load_act(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave);
-      g2_load_weights(nxt, rs, a.G, ltile, b0, g + 1, lane);
-    }
+    // Group g + 1's weights now; its activation rows two loads per k-step
+    // over steps 0-3 below, so that the 64 KiB the workgroup writes into LDS
+    // per group do not arrive in one burst on top of the first steps' operand
+    // reads, and still land half a group before they are needed (measured:
+    // 4% over issuing all eight at once, 1.5% over one per step).
+    const bool more = g + 1 < g1;
+    if (more) g2_load_weights(nxt, rs, a.G, ltile, b0, g + 1, lane);
     float sf[NH], cf[NH];
 #pragma unroll
     for (int j = 0; j < NH; ++j) {
@@ -227,6 +234,10 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int cu = u & 1, nu = cu ^ 1;
+      if (more && u < G2_ACT_LOADS / 2) {
+        g2_load_act1(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u);
+        g2_load_act1(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u + 1);
+      }
       if (u + 1 < 8) {
         const int s1 = (u + 1) >> 2, t1 = (u + 1) & 3;
         const int slot = (8 * s1 + 4 * h + t1) ^ (r & 15);
