@@ -192,6 +192,12 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
   const __amdgpu_buffer_rsrc_t act = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.A) + (size_t)m0 * a.K, 0, (int)((uint32_t)(a.M - m0) * row_bytes),
       0x00020000);
+  const __amdgpu_buffer_rsrc_t act_none =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.A), 0, 0, 0x00020000);
+  const G2Rsrc rs_none = {
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(a.qw), 0, 0, 0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.sc), 0, 0, 0x00020000),
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.zr), 0, 0, 0x00020000)};
   uint32_t voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -212,8 +218,13 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
     // per group do not arrive in one burst on top of the first steps' operand
     // reads, and still land half a group before they are needed (measured:
     // 4% over issuing all eight at once, 1.5% over one per step).
+    // Past the segment's last group the loads go through zero-length
+    // resources: they fetch nothing (out-of-range buffer loads return zeros)
+    // and need no branch, which would split the k-step schedule below.
     const bool more = g + 1 < g1;
-    if (more) g2_load_weights(nxt, rs, a.G, ltile, b0, g + 1, lane);
+    const __amdgpu_buffer_rsrc_t actn = more ? act : act_none;
+    const G2Rsrc rsn = more ? rs : rs_none;
+    g2_load_weights(nxt, rsn, a.G, ltile, b0, g + 1, lane);
     float sf[NH], cf[NH];
 #pragma unroll
     for (int j = 0; j < NH; ++j) {
@@ -234,9 +245,9 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int cu = u & 1, nu = cu ^ 1;
-      if (more && u < G2_ACT_LOADS / 2) {
-        g2_load_act1(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u);
-        g2_load_act1(act, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u + 1);
+      if (u < G2_ACT_LOADS / 2) {
+        g2_load_act1(actn, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u);
+        g2_load_act1(actn, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u + 1);
       }
       if (u + 1 < 8) {
         const int s1 = (u + 1) >> 2, t1 = (u + 1) & 3;
