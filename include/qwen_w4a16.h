@@ -130,7 +130,9 @@ int qw4_choose_splits(int out_f, int num_groups);
 int qw4_tune_decode(int mode, int S, int W, int D, int P);
 /* qw4_tune_gemm: the prefill schedule, -1 the cost model (default), 0 one
  * workgroup per tile, 1 stream-K, 2 hybrid (split schedules need a workspace);
- * variant 0 the default kernel, 2 each wave on a whole 64-row weight tile. */
+ * variant 0 the default kernel (4 waves, each on a whole 64-row weight tile
+ * against all 256 activation rows), 1 8 waves on 32-row tile halves, 2 8 waves
+ * on whole tiles against 128 rows; the variants' results are bitwise equal. */
 int qw4_tune_gemm(int schedule, int variant);
 /* qw4_tune_linear: max_t of qw4_linear for every weight, 0 = the measured rule
  * (the role of the reference's QWEN_MMA_MAX_T environment variable). */

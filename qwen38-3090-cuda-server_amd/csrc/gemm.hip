@@ -49,7 +49,7 @@ namespace {
 //    p = 16 (r % 4) + 8 b + 2 (r / 8) + (r / 4) % 2, so the four D rows a lane
 //    holds for each r / 8 are four consecutive output columns: one 8-byte
 //    store.
-constexpr int G2_BM = 256, G2_BN = 256, G2_MB = G2_BM / 32, G2_WAVES = 8;
+constexpr int G2_BM = 256, G2_BN = 256;
 constexpr int G2_ROWBLOCKS = G2_BM / 4;  // 1 KiB (4-row) activation loads per group
 
 typedef float f32x16v __attribute__((ext_vector_type(16)));
@@ -67,9 +67,33 @@ struct GemmArgs {
   int U;                // (tile, group) units of tiles [full, tiles), split over P
 };
 
-// NH = 1: a wave owns one 32-row tile half against all 8 m-blocks;
-// NH = 2: a wave owns a whole 64-row tile against 4 m-blocks (half the LDS
-// reads per MFMA, every weight dequantized by two waves).
+// Work split of a workgroup's 4 weight tiles x 8 m-blocks over its NW waves:
+//  * NH = 1, NW = 8: a wave owns one 32-row tile half against all 8 m-blocks;
+//  * NH = 2, NW = 8: a wave owns a whole 64-row tile against 4 m-blocks (half
+//    the LDS reads per MFMA, every weight dequantized by two waves);
+//  * NH = 2, NW = 4: one wave per SIMD owns a whole tile against all 8
+//    m-blocks (half the LDS reads, every weight dequantized once; its 256
+//    accumulator registers take the AGPR half of the register file).
+template <int NH, int NW>
+struct G2Split {
+  static constexpr int MBW = 64 / (NW * NH);         // m-blocks per wave
+  static constexpr int UNITS = NH * MBW;             // (half, m-block) pairs per wave
+  static constexpr int ACT = G2_ROWBLOCKS / NW;      // activation loads per wave and group
+  static constexpr int FIXP = 16 / NW;               // fixup blocks per wave region
+  // k-step schedule (measured on MI355X at the config-4 shapes): VALU slots
+  // after each MFMA, LDS operand reads after each of the first MFMAs, and the
+  // k-steps that carry the next group's activation loads.
+  static constexpr int VALU = NW == 8 ? 4 * NH : 2;
+  static constexpr int DS = 2;
+  static constexpr int ACTSTEPS = NW == 8 ? 4 : 8;
+  static_assert(MBW * NH * NW == 64 && ACT % 4 == 0, "unsupported split");
+  __device__ static void coords(int wave, int& wt, int& b0, int& mw) {
+    wt = NH == 1 ? (wave >> 1) : (wave & 3);   // tile of the 4 this wave owns
+    b0 = NH == 1 ? (wave & 1) : 0;             // first tile half
+    mw = NH == 1 ? 0 : (wave >> 2) * MBW;      // first m-block
+  }
+};
+
 template <int NH>
 struct WeightGroup {
   u32x4 q[NH][2];    // [half][s]: chunk 2 s + h of this lane's weight row
@@ -105,24 +129,24 @@ __device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const G2Rsr
   }
 }
 
-// Issue load i (of G2_ROWBLOCKS / G2_WAVES) of this wave's share of the
-// activation rows of group g into buf. `act` covers rows [m0, M); rows past M
-// lie outside it and read as zeros. voff[i % 4] is the lane's byte offset of
-// load i relative to its first row (the swizzle repeats every 4 loads).
-constexpr int G2_ACT_LOADS = G2_ROWBLOCKS / G2_WAVES;   // per wave and group: 8
-static_assert(G2_ACT_LOADS == 8, "two activation loads in each of k-steps 0-3 of a group");
+// Issue load i (of G2_ROWBLOCKS / NW) of this wave's share of the activation
+// rows of group g into buf. `act` covers rows [m0, M); rows past M lie outside
+// it and read as zeros. voff[i % 4] is the lane's byte offset of load i
+// relative to its first row (the swizzle repeats every 4 loads).
+template <int NW>
 __device__ __forceinline__ void g2_load_act1(__amdgpu_buffer_rsrc_t act, const uint32_t (&voff)[4],
                                              uint32_t row_bytes, u32x4* buf, int g, int wave,
                                              int i) {
-  const int rb = wave * G2_ACT_LOADS + i;
+  const int rb = wave * (G2_ROWBLOCKS / NW) + i;
   __builtin_amdgcn_raw_ptr_buffer_load_lds(act, buf + rb * 64, 16,
                                            voff[i & 3] + (uint32_t)(4 * rb) * row_bytes,
                                            (uint32_t)g * (kGroup * 2), 0, 0);
 }
+template <int NW>
 __device__ __forceinline__ void g2_load_act(__amdgpu_buffer_rsrc_t act, const uint32_t (&voff)[4],
                                             uint32_t row_bytes, u32x4* buf, int g, int wave) {
 #pragma unroll
-  for (int i = 0; i < G2_ACT_LOADS; ++i) g2_load_act1(act, voff, row_bytes, buf, g, wave, i);
+  for (int i = 0; i < G2_ROWBLOCKS / NW; ++i) g2_load_act1<NW>(act, voff, row_bytes, buf, g, wave, i);
 }
 
 // One packed word -> 8 bf16 weights RNE((q - z) s), c = -z s, in the order
@@ -173,13 +197,14 @@ __device__ __forceinline__ int g2_xcd_order(int blk, int count) {
 
 // One wave's share of one (tile, group range) segment: acc = sum over groups
 // [g0, g1) of this wave's weight rows x the tile's activation rows.
-template <int NH>
+template <int NH, int NW>
 __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
                                            u32x4 (*lds)[G2_BM * 16],
-                                           f32x16v (&acc)[NH][G2_MB / NH], int m0, int ltile,
-                                           int b0, int mw, int g0, int g1, int wave,
+                                           f32x16v (&acc)[NH][G2Split<NH, NW>::MBW], int m0,
+                                           int ltile, int b0, int mw, int g0, int g1, int wave,
                                            int lane, NibConst kc) {
-  constexpr int MBW = G2_MB / NH;
+  using Sp = G2Split<NH, NW>;
+  constexpr int MBW = Sp::MBW;
   const int r = lane & 31, h = lane >> 5;
   const int zsh = 4 * (r & 3);
 #pragma unroll
@@ -206,15 +231,15 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
     voff[i] = (uint32_t)(lane >> 4) * row_bytes + (uint32_t)c * 16u;
   }
   __syncthreads();   // the previous segment's last LDS reads are done
-  g2_load_act(act, voff, row_bytes, lds[0], g0, wave);
+  g2_load_act<NW>(act, voff, row_bytes, lds[0], g0, wave);
   g2_load_weights(cur, rs, a.G, ltile, b0, g0, lane);
   for (int g = g0; g < g1; ++g) {
     g2_wait_vm0();
     __syncthreads();
     const int sb = (g - g0) & 1;
     const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
-    // Group g + 1's weights now; its activation rows two loads per k-step
-    // over steps 0-3 below, so that the 64 KiB the workgroup writes into LDS
+    // Group g + 1's weights now; its activation rows spread evenly over k-steps
+    // 0-3 below, so that the 64 KiB the workgroup writes into LDS
     // per group do not arrive in one burst on top of the first steps' operand
     // reads, and still land half a group before they are needed (measured:
     // 4% over issuing all eight at once, 1.5% over one per step).
@@ -245,9 +270,11 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int cu = u & 1, nu = cu ^ 1;
-      if (u < G2_ACT_LOADS / 2) {
-        g2_load_act1(actn, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u);
-        g2_load_act1(actn, voff, row_bytes, lds[sb ^ 1], g + 1, wave, 2 * u + 1);
+      if (u < Sp::ACTSTEPS) {
+#pragma unroll
+        for (int i = 0; i < Sp::ACT / Sp::ACTSTEPS; ++i)
+          g2_load_act1<NW>(actn, voff, row_bytes, lds[sb ^ 1], g + 1, wave,
+                           Sp::ACT / Sp::ACTSTEPS * u + i);
       }
       if (u + 1 < 8) {
         const int s1 = (u + 1) >> 2, t1 = (u + 1) & 3;
@@ -267,10 +294,14 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
         for (int i = 0; i < MBW * NH; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-          if (i < MBW / 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-          __builtin_amdgcn_sched_group_barrier(0x002, 4 * NH, 0);  // VALU
+          if (i < MBW / Sp::DS) __builtin_amdgcn_sched_group_barrier(0x100, Sp::DS, 0);  // DS read
+          __builtin_amdgcn_sched_group_barrier(0x002, Sp::VALU, 0);  // VALU
         }
       }
+      // NW = 4: one scheduling region per k-step, so that the next step's
+      // operand reads stay under this step's MFMAs instead of sinking to their
+      // first use (with one wave per SIMD nothing else hides their latency).
+      if (NW == 4) __builtin_amdgcn_sched_barrier(0);
     }
     cur = nxt;
   }
@@ -278,10 +309,11 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 
 // D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
 // columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
-template <int NH>
-__device__ __forceinline__ void g2_store(const GemmArgs& a, const f32x16v (&acc)[NH][G2_MB / NH],
-                                         int m0, int tile, int b0, int mw, int lane) {
-  constexpr int MBW = G2_MB / NH;
+template <int NH, int NW>
+__device__ __forceinline__ void g2_store(const GemmArgs& a,
+                                         const f32x16v (&acc)[NH][G2Split<NH, NW>::MBW], int m0,
+                                         int tile, int b0, int mw, int lane) {
+  constexpr int MBW = G2Split<NH, NW>::MBW;
   const int r = lane & 31, h = lane >> 5;
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
@@ -307,21 +339,23 @@ __device__ __forceinline__ void g2_store(const GemmArgs& a, const f32x16v (&acc)
 // stores the tile.
 constexpr uint32_t kSlotBytes = (uint32_t)G2_BM * G2_BN * 4;   // 256 KiB
 
-__device__ __forceinline__ uint32_t g2_slot_off(int vp, int which, int wave, int mb, int lane) {
+// idx: the wave's (half, m-block) pair j * MBW + mb, of `units` per wave.
+__device__ __forceinline__ uint32_t g2_slot_off(int vp, int which, int wave, int units, int idx,
+                                                int lane) {
   return (uint32_t)(vp * 2 + which) * kSlotBytes +
-         (uint32_t)(((wave * G2_MB + mb) * 64 + lane) * 64);
+         (uint32_t)(((wave * units + idx) * 64 + lane) * 64);
 }
 
-template <int NH>
+template <int NH, int NW>
 __device__ __forceinline__ void g2_slot_store(__amdgpu_buffer_rsrc_t rs,
-                                              const f32x16v (&acc)[NH][G2_MB / NH], int vp,
-                                              int which, int wave, int lane) {
-  constexpr int MBW = G2_MB / NH;
+                                              const f32x16v (&acc)[NH][G2Split<NH, NW>::MBW],
+                                              int vp, int which, int wave, int lane) {
+  constexpr int MBW = G2Split<NH, NW>::MBW;
 #pragma unroll
   for (int j = 0; j < NH; ++j)
 #pragma unroll
     for (int mb = 0; mb < MBW; ++mb) {
-      const uint32_t off = g2_slot_off(vp, which, wave, j * MBW + mb, lane);
+      const uint32_t off = g2_slot_off(vp, which, wave, NH * MBW, j * MBW + mb, lane);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4 v = {__float_as_uint(acc[j][mb][4 * i]), __float_as_uint(acc[j][mb][4 * i + 1]),
@@ -342,27 +376,28 @@ __device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
 }
 
 // The cut tiles' fp32 partials are summed by many small blocks: block
-// (tile ts, main-kernel wave w, part) owns the m-blocks [part * 4, part * 4 + 4)
-// of wave w's region (the slot layout [wave][m-block][lane] keeps them
+// (tile ts, main-kernel wave w, part) owns the pairs [part * 4, part * 4 + 4)
+// of wave w's region (the slot layout [wave][pair][lane] keeps them
 // contiguous), so a cut tile is read by 16 blocks at once instead of one
 // workgroup. Tiles a single workgroup covered were stored by the main kernel.
-constexpr int kFixParts = 2;   // parts per main-kernel wave region
+constexpr int kFixBlocksPerTile = 16;
 
-template <int NH>
+template <int NH, int NW>
 __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
-  constexpr int MBW = G2_MB / NH;
-  constexpr int kPer = G2_MB / kFixParts;   // (half, m-block) pairs per block
-  const int ts = blockIdx.x / (G2_WAVES * kFixParts);   // split tile full + ts
-  const int wave = (blockIdx.x / kFixParts) % G2_WAVES;
-  const int part = blockIdx.x % kFixParts;
+  using Sp = G2Split<NH, NW>;
+  constexpr int MBW = Sp::MBW;
+  constexpr int kPer = Sp::UNITS / Sp::FIXP;   // (half, m-block) pairs per block
+  static_assert(NW * Sp::FIXP == kFixBlocksPerTile && kPer == 4, "fixup split");
+  const int ts = blockIdx.x / kFixBlocksPerTile;   // split tile full + ts
+  const int wave = (blockIdx.x / Sp::FIXP) % NW;
+  const int part = blockIdx.x % Sp::FIXP;
   const int t = a.full + ts;
   const int p0 = g2_owner_of(a, ts * a.G), p1 = g2_owner_of(a, ts * a.G + a.G - 1);
   if (p0 == p1) return;
   const int lane = threadIdx.x & 63;
   const int r = lane & 31, h = lane >> 5;
-  const int wt = NH == 1 ? (wave >> 1) : (wave & 3);
-  const int b0 = NH == 1 ? (wave & 1) : 0;
-  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;
+  int wt, b0, mw;
+  Sp::coords(wave, wt, b0, mw);
   int tn, tm;
   g2_tile_coords(a, t, tn, tm);
   const int tile = tn * 4 + wt;
@@ -376,7 +411,7 @@ __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
     const int which = (g2_range_start(a, pp) / a.G == ts) ? 0 : 1;
 #pragma unroll
     for (int e = 0; e < kPer; ++e) {
-      const uint32_t off = g2_slot_off(pp, which, wave, part * kPer + e, lane);
+      const uint32_t off = g2_slot_off(pp, which, wave, Sp::UNITS, part * kPer + e, lane);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
@@ -402,15 +437,15 @@ __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
   }
 }
 
-template <int NH>
-__global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
-  constexpr int MBW = G2_MB / NH;           // m-blocks per wave
+template <int NH, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
+  using Sp = G2Split<NH, NW>;
+  constexpr int MBW = Sp::MBW;              // m-blocks per wave
   __shared__ u32x4 lds[2][G2_BM * 16];      // 2 x 64 KiB: [row][16 swizzled chunks]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int lane = threadIdx.x & 63;
-  const int wt = NH == 1 ? (wave >> 1) : (wave & 3);   // tile of the 4 this wave owns
-  const int b0 = NH == 1 ? (wave & 1) : 0;
-  const int mw = NH == 1 ? 0 : (wave >> 2) * MBW;      // first m-block of this wave
+  int wt, b0, mw;
+  Sp::coords(wave, wt, b0, mw);
   const NibConst kc = nib_const();
   f32x16v acc[NH][MBW];
 
@@ -437,8 +472,8 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
     const int tile = tn * 4 + wt;
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
-    g2_segment<NH>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane, kc);
-    if (valid) g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane, kc);
+    if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
   }
   for (int u = u0; u < u1;) {
     const int ts = u / a.G, g0 = u - ts * a.G;
@@ -448,11 +483,11 @@ __global__ __launch_bounds__(512, 1) void k_gemm(GemmArgs a) {
     const int tile = tn * 4 + wt;
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
-    g2_segment<NH>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane, kc);
+    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane, kc);
     if (g0 == 0 && g1 == a.G) {
-      if (valid) g2_store<NH>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+      if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
     } else {
-      g2_slot_store<NH>(rs, acc, vp, u == u0 ? 0 : 1, wave, lane);
+      g2_slot_store<NH, NW>(rs, acc, vp, u == u0 ? 0 : 1, wave, lane);
     }
     u = ts * a.G + g1;
   }
@@ -478,7 +513,11 @@ int device_cus() {
 // Tuning and test override of the prefill schedule (qw4_tune_gemm): -1 the
 // cost model, 0 per tile, 1 stream-K, 2 hybrid.
 std::atomic<int> g_gemm_schedule{-1};
-std::atomic<int> g_gemm_nh{1};   // weight rows per wave: 1 = 32-row halves, 2 = 64-row tiles
+// Kernel variant (qw4_tune_gemm): 0 the default, 4 waves of whole 64-row
+// tiles against all 256 activation rows; 1 8 waves of 32-row tile halves; 2 8
+// waves of whole tiles against 128 rows. All three sum every output in the
+// same order, so their results are bitwise equal.
+std::atomic<int> g_gemm_variant{0};
 
 }  // namespace
 }  // namespace qw4
@@ -512,7 +551,7 @@ int qw4_workspace_free(qw4_workspace* ws) {
 int qw4_tune_gemm(int schedule, int variant) {
   if (schedule < -1 || schedule > 2 || variant < 0 || variant > 2) return QW4_ERR_SHAPE;
   g_gemm_schedule.store(schedule, std::memory_order_relaxed);
-  g_gemm_nh.store(variant == 2 ? 2 : 1, std::memory_order_relaxed);
+  g_gemm_variant.store(variant, std::memory_order_relaxed);
   return QW4_OK;
 }
 
@@ -574,18 +613,22 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
       grid = cus;
     }
     hipStream_t s = (hipStream_t)stream;
-    const int nh = g_gemm_nh.load(std::memory_order_relaxed);
-    if (nh == 2)
-      k_gemm<2><<<grid, 512, 0, s>>>(a);
+    const int variant = g_gemm_variant.load(std::memory_order_relaxed);
+    if (variant == 1)
+      k_gemm<1, 8><<<grid, 512, 0, s>>>(a);
+    else if (variant == 2)
+      k_gemm<2, 8><<<grid, 512, 0, s>>>(a);
     else
-      k_gemm<1><<<grid, 512, 0, s>>>(a);
+      k_gemm<2, 4><<<grid, 256, 0, s>>>(a);
     QW4_LAUNCH_CHECK();
     if (a.full != nt) {   // the split tiles
-      const int fb = (nt - a.full) * G2_WAVES * kFixParts;
-      if (nh == 2)
-        k_gemm_fixup<2><<<fb, 64, 0, s>>>(a);
+      const int fb = (nt - a.full) * kFixBlocksPerTile;
+      if (variant == 1)
+        k_gemm_fixup<1, 8><<<fb, 64, 0, s>>>(a);
+      else if (variant == 2)
+        k_gemm_fixup<2, 8><<<fb, 64, 0, s>>>(a);
       else
-        k_gemm_fixup<1><<<fb, 64, 0, s>>>(a);
+        k_gemm_fixup<2, 4><<<fb, 64, 0, s>>>(a);
     }
     QW4_LAUNCH_CHECK();
     return QW4_OK;

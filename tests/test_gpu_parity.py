@@ -295,6 +295,36 @@ def test_prefill_gemm_vs_oracle(hip, orc, gemm_ws, M, N, K, use_ws):
     hip.awq_free(w)
 
 
+@pytest.mark.parametrize("M,N,K", [(777, 5184, 4096), (64, 896, 640), (1100, 17408, 5120),
+                                   (1024, 5120, 17408)])
+def test_prefill_kernel_variants_bitwise(hip, orc, gemm_ws, M, N, K):
+    """The three prefill kernels (the default 4 waves of whole 64-row tiles, 8
+    waves of tile halves, 8 waves of whole tiles against half the rows) sum
+    every output in the same order: under each schedule (per tile, stream-K,
+    hybrid) their results are bitwise equal. The default is checked against
+    the oracle above."""
+    import torch
+
+    q, zp, s = orc.gen_weights(N, K, seed=M + 5)
+    x = orc.gen_x(M, K, seed=M + 5)
+    w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
+    dx = dev(x)
+    try:
+        for sched in (0, 1, 2):
+            outs = []
+            for variant in (0, 1, 2):
+                hip.tune_gemm(sched, variant)
+                y = empty((M, N), np.uint16)
+                hip.gemm_w4a16(y, w, dx, M, gemm_ws)
+                outs.append(y)
+            torch.cuda.synchronize()
+            for variant in (1, 2):
+                assert torch.equal(outs[0], outs[variant]), f"schedule {sched} variant {variant}"
+    finally:
+        hip.tune_gemm(-1, 0)
+    hip.awq_free(w)
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 17408, 5120), (4096, 5120, 17408), (1024, 17408, 5120),
                                    (1024, 5120, 17408)])
 def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
