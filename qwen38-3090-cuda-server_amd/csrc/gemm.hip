@@ -79,7 +79,7 @@ struct G2Split {
   static constexpr int MBW = 64 / (NW * NH);         // m-blocks per wave
   static constexpr int UNITS = NH * MBW;             // (half, m-block) pairs per wave
   static constexpr int ACT = G2_ROWBLOCKS / NW;      // activation loads per wave and group
-  static constexpr int FIXP = 16 / NW;               // fixup blocks per wave region
+  static constexpr int FIXP = 32 / NW;               // fixup blocks per wave region
   // k-step schedule (measured on MI355X at the config-4 shapes): VALU slots
   // after each MFMA, LDS operand reads after each of the first MFMAs, and the
   // k-steps that carry the next group's activation loads.
@@ -376,18 +376,22 @@ __device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
 }
 
 // The cut tiles' fp32 partials are summed by many small blocks: block
-// (tile ts, main-kernel wave w, part) owns the pairs [part * 4, part * 4 + 4)
+// (tile ts, main-kernel wave w, part) owns the pairs [part * 2, part * 2 + 2)
 // of wave w's region (the slot layout [wave][pair][lane] keeps them
-// contiguous), so a cut tile is read by 16 blocks at once instead of one
-// workgroup. Tiles a single workgroup covered were stored by the main kernel.
-constexpr int kFixBlocksPerTile = 16;
+// contiguous), so a cut tile is read by 32 blocks at once instead of one
+// workgroup. A block loads kFixAhead pieces before it adds them, in piece
+// order, so that the loads of a tile split many ways overlap instead of
+// paying one memory latency per piece. Tiles a single workgroup covered were
+// stored by the main kernel.
+constexpr int kFixBlocksPerTile = 32;
+constexpr int kFixAhead = 4;
 
 template <int NH, int NW>
 __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
   using Sp = G2Split<NH, NW>;
   constexpr int MBW = Sp::MBW;
   constexpr int kPer = Sp::UNITS / Sp::FIXP;   // (half, m-block) pairs per block
-  static_assert(NW * Sp::FIXP == kFixBlocksPerTile && kPer == 4, "fixup split");
+  static_assert(NW * Sp::FIXP == kFixBlocksPerTile && kPer == 2, "fixup split");
   const int ts = blockIdx.x / kFixBlocksPerTile;   // split tile full + ts
   const int wave = (blockIdx.x / Sp::FIXP) % NW;
   const int part = blockIdx.x % Sp::FIXP;
@@ -407,17 +411,33 @@ __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
   f32x16v acc[kPer];
 #pragma unroll
   for (int e = 0; e < kPer; ++e) acc[e] = f32x16v{};
-  for (int pp = p0; pp <= p1; ++pp) {
-    const int which = (g2_range_start(a, pp) / a.G == ts) ? 0 : 1;
+  for (int pp = p0; pp <= p1; pp += kFixAhead) {
+    u32x4 v[kFixAhead][kPer][4];
 #pragma unroll
-    for (int e = 0; e < kPer; ++e) {
-      const uint32_t off = g2_slot_off(pp, which, wave, Sp::UNITS, part * kPer + e, lane);
+    for (int k = 0; k < kFixAhead; ++k) {
+      // pieces past p1 read out of range (zeros, no memory access) and are
+      // never added: adding +0 would turn a -0 sum into +0
+      const int q = pp + k;
+      const bool live = q <= p1;
+      const int which = (live && g2_range_start(a, q) / a.G == ts) ? 0 : 1;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+      for (int e = 0; e < kPer; ++e) {
+        const uint32_t off =
+            live ? g2_slot_off(q, which, wave, Sp::UNITS, part * kPer + e, lane) : 0x80000000u;
 #pragma unroll
-        for (int c = 0; c < 4; ++c) acc[e][4 * i + c] += __uint_as_float(v[c]);
+        for (int i = 0; i < 4; ++i)
+          v[k][e][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
       }
+    }
+#pragma unroll
+    for (int k = 0; k < kFixAhead; ++k) {
+      if (pp + k > p1) break;
+#pragma unroll
+      for (int e = 0; e < kPer; ++e)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) acc[e][4 * i + c] += __uint_as_float(v[k][e][i][c]);
     }
   }
   // pair index j * MBW + mb (g2_slot_store's order)
