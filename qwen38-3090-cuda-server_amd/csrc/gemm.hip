@@ -26,9 +26,10 @@ int check_weights_public(const qw4_weights* w);
 namespace {
 
 // ---------------------------------------------------------------------------
-// k_gemm: 256 (M) x 256 (N) workgroup tile, 8 waves (two per SIMD), each wave
-// one 32-row half of a 64-row weight tile against all 256 activation rows,
-// v_mfma_f32_32x32x16_bf16 (the full-rate bf16 shape on gfx950).
+// k_gemm: 256 (M) x 256 (N) workgroup tile, v_mfma_f32_32x32x16_bf16 (the
+// full-rate bf16 shape on gfx950). The default: 4 waves, one per SIMD, each a
+// whole 64-row weight tile against all 256 activation rows (its 256
+// accumulator registers in AGPRs); G2Split below lists the 8-wave forms.
 //
 //  * Weights are the MFMA A operand (rows = output columns n). Each wave loads
 //    its packed rows straight into registers -- 32 B per lane per group, one
