@@ -203,7 +203,7 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
                                            u32x4 (*lds)[G2_BM * 16],
                                            f32x16v (&acc)[NH][G2Split<NH, NW>::MBW], int m0,
                                            int ltile, int b0, int mw, int g0, int g1, int wave,
-                                           int lane, NibConst kc) {
+                                           int lane) {
   using Sp = G2Split<NH, NW>;
   constexpr int MBW = Sp::MBW;
   const int r = lane & 31, h = lane >> 5;
@@ -239,11 +239,11 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
     __syncthreads();
     const int sb = (g - g0) & 1;
     const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
-    // Group g + 1's weights now; its activation rows spread evenly over k-steps
-    // 0-3 below, so that the 64 KiB the workgroup writes into LDS
-    // per group do not arrive in one burst on top of the first steps' operand
-    // reads, and still land half a group before they are needed (measured:
-    // 4% over issuing all eight at once, 1.5% over one per step).
+    // Group g + 1's weights now; its activation rows spread evenly over the
+    // first Sp::ACTSTEPS k-steps below, so that the 64 KiB the workgroup writes
+    // into LDS per group do not arrive in one burst on top of the first steps'
+    // operand reads (8 waves: steps 0-3, 4% faster than one burst and 1.5%
+    // than one load per step; 4 waves: all 8 steps, equal to steps 0-3).
     // Past the segment's last group the loads go through zero-length
     // resources: they fetch nothing (out-of-range buffer loads return zeros)
     // and need no branch, which would split the k-step schedule below.
@@ -467,7 +467,6 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
   const int lane = threadIdx.x & 63;
   int wt, b0, mw;
   Sp::coords(wave, wt, b0, mw);
-  const NibConst kc = nib_const();
   f32x16v acc[NH][MBW];
 
   // Virtual workgroup vp (XCD x owns a contiguous run of vp) first does the
@@ -493,7 +492,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
     const int tile = tn * 4 + wt;
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
-    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane, kc);
+    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane);
     if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
   }
   for (int u = u0; u < u1;) {
@@ -504,7 +503,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
     const int tile = tn * 4 + wt;
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
-    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane, kc);
+    g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane);
     if (g0 == 0 && g1 == a.G) {
       if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
     } else {
