@@ -1386,16 +1386,18 @@ constexpr int kDecCount = (int)(sizeof(kDecAll) / sizeof(kDecAll[0]));
 
 // Returns false when the shape does not fit k_dec (activations beyond the
 // per-wave prep, LDS beyond the CU's). Policy, measured on MI355X over the
-// config-2 projections (32-row units throughout; 16-row units and deeper
-// items were slower): 2 items per wave for short K (o_proj, 32 groups), 16
-// waves of 2 items when the output has fewer tiles than CUs and K is long
-// (down: 160 workgroups), else 8 waves of 3 items.
+// config-2 projections with every variant forced in one process (32-row
+// units throughout; 16-row units and deeper items were slower): when the
+// output has fewer tiles than CUs, 2 items per wave, 16 waves for long K
+// (down: 10.9 us against 11.3 for 8 x 3), 8 for short (qkv: 5.7 against
+// 6.0; o_proj 4.9 against 5.0); else 2 items per wave for short K (32
+// groups) and 8 waves of 3 items otherwise (gate|up).
 bool dec_config(int out_f, int G, int OUTmode, DecCfg& c) {
   const int tiles = out_f / kTileN;
   const int K = G * kGroup;
-  DecVariant v = (tiles < device_cus() && G >= 64) ? kDecAll[2]
-                 : G <= 32                          ? kDecAll[1]
-                                                    : kDecAll[0];
+  DecVariant v = tiles < device_cus() ? (G >= 64 ? kDecAll[2] : kDecAll[1])
+                 : G <= 32            ? kDecAll[1]
+                                      : kDecAll[0];
   if (OUTmode == OUT_BF16 && g_dec_tune.mode.load(std::memory_order_relaxed) == 3) {
     const int tS = g_dec_tune.S.load(std::memory_order_relaxed);
     const int tW = g_dec_tune.W.load(std::memory_order_relaxed);
