@@ -134,3 +134,55 @@ def test_linear_threshold_by_weight_size(hip):
     finally:
         hip.tune_linear(0)
     assert hip.linear_max_t(w) == want[(n, k)]
+
+
+def test_host_paths_from_many_threads(hip):
+    """The host-side launch policy and argument checks called from many threads
+    at once (ctypes releases the GIL, so the calls overlap): every thread gets
+    the single-threaded answers. The per-device caches behind them are filled
+    under std::call_once or are atomics (the reference's lazy statics,
+    gemv_w4a16.cu:281-297, would race here)."""
+    import threading
+
+    L = hip.lib()
+    hip.tune_linear(0)
+    shapes = [(34816, 5120), (5120, 17408), (7168, 5120), (5120, 4096)]
+
+    def answers():
+        out = []
+        for n, k in shapes:
+            w = hip.W4A16Weights()
+            w.out_f, w.in_f, w.group_size, w.num_groups = n, k, 128, k // 128
+            out.append(hip.linear_max_t(w))
+            out.append(hip.gemv_choose_splits(n, k // 128))
+        w, s = _fake_weights(hip), _fake_scratch(hip)
+        x, y = C.c_void_p(0x10000), C.c_void_p(0x20000)
+        out.append(L.qw4_gemm_small(y, C.byref(w), x, 17, C.byref(s), None))
+        out.append(L.qw4_gemv(y, C.byref(_fake_weights(hip, group=64)), x, C.byref(s), None))
+        out.append(L.qw4_gemv(y, C.byref(w), C.c_void_p(0x10002), C.byref(s), None))
+        out.append(L.qw4_status_string(hip.QW4_ERR_SHAPE))
+        return out
+
+    want = answers()
+    got, errors = [None] * 16, []
+    start = threading.Barrier(16)
+
+    def work(i):
+        try:
+            start.wait()
+            for _ in range(50):
+                r = answers()
+                if r != want:
+                    got[i] = r
+                    return
+            got[i] = want
+        except Exception as e:   # reported by the main thread
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(16)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    assert all(g == want for g in got), got
