@@ -244,6 +244,9 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
 // (no item registers).
 constexpr int kRowsXChunks = 4;
 constexpr int rows_xchunks(bool dma) { return dma ? 2 * kRowsXChunks : kRowsXChunks; }
+// k_rows with LDS-DMA items and M > 1 rows staged (XM, 8 waves): at most this
+// many 16-byte chunks per thread
+constexpr int kRowsXmChunks = 16;
 constexpr int kLdsBytes = 160 * 1024;   // LDS per CU on gfx950
 
 
@@ -506,14 +509,19 @@ __device__ __forceinline__ void emit_swiglu(const SkinnyArgs& a, int b, int st0,
 // only those lanes take part in the unit sums and only that element is
 // accumulated; without (M > 1) each item's activations still go to registers,
 // loaded with the item.
-template <int OUT, int FMT, int S, int W, bool XL, int D, bool DMA = false>
+template <int OUT, int FMT, int S, int W, bool XL, int D, bool DMA = false, bool XM = false>
 __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
-  constexpr bool kM1 = DMA && XL;   // LDS-DMA items with staged activations: M = 1
+  // LDS-DMA items with staged activations: M = 1, or (XM) M > 1 with each
+  // activation row padded by one 16-byte chunk, so that the 16 lanes reading
+  // one k-chunk of 16 different rows hit different banks
+  static_assert(!XM || (DMA && XL && OUT != OUT_NORM), "XM: staged rows, LDS-DMA items");
+  constexpr bool kM1 = DMA && XL && !XM;
   constexpr uint32_t kPer = 4 / S;   // units per tile (unit indices are never negative)
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
   constexpr int kRedLanes = kM1 ? 16 : 64;
-  constexpr int kXC = rows_xchunks(DMA);
-  __shared__ f32x4 red[2][W][S][kRedLanes];
+  constexpr int kRedBufs = XM ? 1 : 2;   // XM: one buffer (LDS), a second barrier per unit
+  constexpr int kXC = XM ? kRowsXmChunks : rows_xchunks(DMA);
+  __shared__ f32x4 red[kRedBufs][W][S][kRedLanes];
   extern __shared__ u32x4 xlds[];
   // wave-uniform (scalar) so the item cursors live in SGPRs
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -557,7 +565,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   };
 
   RowsData<FMT, S, XL> buf[kM1 ? 1 : D];
-  u32x4* const ring = xlds + (XL ? a.M * a.K / 8 : 0) + wave * D * DmaSlot<FMT, S>::kUnits;
+  const int xs16 = a.K / 8 + (XM ? 1 : 0);   // staged row stride, 16-byte chunks
+  u32x4* const ring = xlds + (XL ? a.M * xs16 : 0) + wave * D * DmaSlot<FMT, S>::kUnits;
   auto load_slot = [&](int j) __attribute__((always_inline)) {
     const bool in = lu < u1;
     const int ru = real_unit(lu);
@@ -579,7 +588,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
       ++lu;
     }
   };
-  const u32x4* xrow = xlds + ((c < a.M ? c : a.M - 1) * a.K + 32 * q) / 8;
+  const u32x4* xrow = xlds + (c < a.M ? c : a.M - 1) * xs16 + 4 * q;
   auto prime = [&]() {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
@@ -611,7 +620,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     prime();
 #pragma unroll
-    for (int j = 0; j < kXC; ++j) xlds[xi[j]] = xv[j];
+    for (int j = 0; j < kXC; ++j) xlds[XM ? xi[j] + xi[j] / (a.K / 8) : xi[j]] = xv[j];
     lds_barrier<DMA>();
     if (OUT == OUT_NORM) {
       // rmsnorm of each row in place (src/kernels/elementwise.cu:8-31):
@@ -659,17 +668,17 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   auto close_unit = [&]() {
     if (!kM1 || lane < kRedLanes) {
 #pragma unroll
-      for (int i = 0; i < S; ++i) red[par][wave][i][lane % kRedLanes] = acc[i];
+      for (int i = 0; i < S; ++i) red[par % kRedBufs][wave][i][lane % kRedLanes] = acc[i];
     }
     lds_barrier<DMA>();
     if (wave == 0) {
       const int rl = lane % kRedLanes;
       f32x4 t[S];
 #pragma unroll
-      for (int i = 0; i < S; ++i) t[i] = red[par][0][i][rl];
+      for (int i = 0; i < S; ++i) t[i] = red[par % kRedBufs][0][i][rl];
       for (int w = 1; w < W; ++w)
 #pragma unroll
-        for (int i = 0; i < S; ++i) t[i] += red[par][w][i][rl];
+        for (int i = 0; i < S; ++i) t[i] += red[par % kRedBufs][w][i][rl];
       if (OUT == OUT_SWIGLU) {
         const int gu = closed >> 1;   // the gate unit (= the output unit)
         if ((closed & 1) == 0) {
@@ -687,6 +696,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
                           lane, bs);
       }
     }
+    if (kRedBufs == 1) lds_barrier<DMA>();   // wave 0 has read the buffer
     par ^= 1;
     ++closed;
 #pragma unroll
@@ -1168,7 +1178,8 @@ int device_cus() {
 struct DecTune {
   // 0 policy; 1 k_rows for M = 1 too (S forces the unit size, D the LDS-DMA
   // depth 2..4); 2 k_rows with register items (S / W force unit size, waves);
-  // 3 k_dec of the given S / W / D (OUT_BF16)
+  // 3 k_dec of the given S / W / D (OUT_BF16); 4 the policy, but M > 1 rows
+  // never staged in LDS (activations loaded with each item)
   std::atomic<int> mode{0};
   std::atomic<int> S{0}, W{0}, D{0}, P{0};
 };
@@ -1179,6 +1190,7 @@ struct Launch {
   int S;         // units of S row quads
   bool XL;       // activations staged in LDS
   int DMA = 0;   // items in LDS slots, this many per wave (0: registers)
+  bool XM = false;   // DMA with M > 1 rows staged (padded rows)
 };
 
 // Items each k_rows wave keeps in flight (the one being computed included),
@@ -1262,9 +1274,11 @@ int rows_occ(int S, bool xl) {
 //    units and 8 waves, 4 items per wave when the output has at least 1.5
 //    64-row tiles per CU, 3 for long K (>= 64 groups), else 2; the fused
 //    rmsnorm and the 8-bit head run faster with register items.
-//  * M > 1 (verify, heads): weight items in slots, activations loaded with
-//    each item, units of the register policy's size, 2 items per wave (3% /
-//    5% per layer at M = 9 / 16 over register items; deeper was slower).
+//  * M > 1 (verify, heads): weight items in slots, 2 items per wave;
+//    activations staged in LDS (padded rows, 32-row units) when they fit and
+//    the workgroups own several units each, else loaded with each item in
+//    units of the register policy's size (3% / 5% per layer at M = 9 / 16
+//    over register items; deeper was slower).
 // Tuning override (qw4_tune_decode): mode 2 keeps register items everywhere
 // (S / W force unit size and waves), mode 1 forces the LDS-DMA depth.
 template <int OUT, int FMT>
@@ -1317,6 +1331,26 @@ Launch launch_for(int out_f, int G, int M) {
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, pc2));
     }
   } else if (M > 1 && OUT != OUT_NORM && l.S != 1) {
+    // All M rows staged in LDS once (padded rows, 32-row units, 2 items per
+    // wave, one reduction buffer) when they fit and the workgroups own more
+    // than one unit on average: the per-item loads re-read x once per unit.
+    // Measured on MI355X, both forms in one process: gate|up at M = 9 (4.25
+    // units per workgroup) 22.3 against 24.1 us; with one unit per workgroup
+    // (qkv, o_proj) within +-5% either way, so those keep the per-item loads.
+    const int xm_need = M * (G * kGroup * 2 + 16) +
+                        8 * 2 * ((FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256)) +
+                        8 * 2 * 64 * 16 + 512;
+    if (mode != 1 && mode != 4 && 2LL * tiles > cus && M * G * kGroup / 8 <= kRowsXmChunks * 64 * 8 &&
+        xm_need <= kLdsBytes) {
+      l.DMA = 2;
+      l.S = 2;
+      l.W = 8;
+      l.XL = true;
+      l.XM = true;
+      const long long u2 = (long long)tiles * 2;
+      l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, (long long)cus));
+      return l;
+    }
     const int S = l.S;
     const int dd = (mode == 1 && tD >= 2 && tD <= 4 && !(OUT == OUT_ARGMAX && S == 4)) ? tD : 2;
     const int slot = (FMT == 8 ? 2 * S : S) * 1024 + (FMT == 4 ? 512 : 256);
@@ -1456,17 +1490,17 @@ void prepare_dec() {
   prepare_dec_i<OUT, 0>();
 }
 
-template <int OUT, int FMT, int S, int W, int D, bool XL>
+template <int OUT, int FMT, int S, int W, int D, bool XL, bool XM = false>
 void launch_rows_dma_d(const SkinnyArgs& a, hipStream_t st) {
-  const int lds = (XL ? a.M * a.K * 2 : 0) + W * D * DmaSlot<FMT, S>::kUnits * 16;
-  constexpr auto kern = &k_rows<OUT, FMT, S, W, XL, D, true>;
+  const int lds = (XL ? a.M * (a.K * 2 + (XM ? 16 : 0)) : 0) + W * D * DmaSlot<FMT, S>::kUnits * 16;
+  constexpr auto kern = &k_rows<OUT, FMT, S, W, XL, D, true, XM>;
   allow_lds<kern>(lds);
   kern<<<a.P, 64 * W, lds, st>>>(a);
 }
 
-template <int OUT, int FMT, int S, bool XL, int D>
+template <int OUT, int FMT, int S, bool XL, int D, bool XM = false>
 void prepare_dma_one() {
-  constexpr auto kern = &k_rows<OUT, FMT, S, 8, XL, D, true>;
+  constexpr auto kern = &k_rows<OUT, FMT, S, 8, XL, D, true, XM>;
   hipFuncAttributes at{};
   if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kern)) == hipSuccess)
     allow_lds<kern>(kLdsBytes - (int)at.sharedSizeBytes);
@@ -1479,6 +1513,7 @@ void prepare_dma_out() {
   prepare_dma_one<OUT, FMT, 2, true, 3>();
   prepare_dma_one<OUT, FMT, 2, true, 4>();
   if constexpr (OUT != OUT_NORM) {
+    prepare_dma_one<OUT, FMT, 2, true, 2, true>();
     prepare_dma_one<OUT, FMT, 2, false, 2>();
     prepare_dma_one<OUT, FMT, 2, false, 3>();
     prepare_dma_one<OUT, FMT, 2, false, 4>();
@@ -1529,6 +1564,12 @@ void launch_rows_dma(const SkinnyArgs& a, int D, hipStream_t st) {
 template <int OUT, int FMT>
 void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
   if (l.DMA) {
+    if constexpr (OUT != OUT_NORM) {
+      if (l.XM) {   // M > 1 rows staged: 2 items per wave (launch_for)
+        launch_rows_dma_d<OUT, FMT, 2, 8, 2, true, true>(a, st);
+        return;
+      }
+    }
     if (l.XL)
       launch_rows_dma<OUT, FMT, 2, true>(a, l.DMA, st);
     else if constexpr (OUT != OUT_NORM) {

@@ -24,9 +24,11 @@ def orc():
 @pytest.fixture(params=["dec", "rows", "regs"])
 def decode_path(request):
     """Runs a decode/verify test through every skinny kernel form: the default
-    (M = 1: the integer-MFMA k_dec; M > 1: k_rows with LDS-DMA items), k_rows
-    at M = 1 too, and k_rows with items in registers for every M, through the
-    library's tuning override (qw4_tune_decode), reset afterwards."""
+    (M = 1: the integer-MFMA k_dec; M > 1: k_rows with LDS-DMA items, the
+    activation rows staged in LDS where the policy stages them), k_rows at
+    M = 1 too with the M > 1 activations loaded with each item, and k_rows
+    with items in registers for every M, through the library's tuning
+    override (qw4_tune_decode), reset afterwards."""
     import w4a16_hip as hip
 
     hip.tune_decode({"dec": 0, "rows": 1, "regs": 2}[request.param])

@@ -296,3 +296,76 @@ def test_dma_w8_verify(hip, scratch, M):
         _both_m(hip, gemm, rows)
         _both_m(hip, argmax, rows)
     hip.w8a16_free(w)
+
+
+# ------------------------------------------- M > 1 with the rows staged in LDS
+def _staged_vs_per_item(hip, run):
+    """run() with the policy (the activation rows staged in LDS where they fit
+    and the workgroups own several units), with per-item activation loads
+    (qw4_tune_decode mode 4) and with register items (mode 2): every result
+    equal. The per-row sums run over the same groups in the same wave order in
+    every form, so any difference is a staging, padding or wait error."""
+    try:
+        hip.tune_decode(0)
+        want = run()
+        for mode in (4, 2):
+            hip.tune_decode(mode)
+            got = run()
+            assert np.array_equal(got, want), mode
+    finally:
+        hip.tune_decode(0)
+
+
+# gate|up (544 tiles), a head-like 16384-row output, a short-K one; the 5120-row
+# output has fewer tiles than half the CUs and keeps the per-item loads
+STAGED = [(34816, 5120), (16384, 1024), (20480, 384), (5120, 4096)]
+
+
+@pytest.mark.parametrize("M", [2, 9, 12, 16])
+@pytest.mark.parametrize("N,K", STAGED)
+def test_staged_rows(hip, scratch, N, K, M):
+    w, x, h0 = _gen(hip, N, K, seed=N + M), _x(hip, M * K, 900 + M), _x(hip, M * N, 901)
+    print(f"staged rows M={M} {N}x{K}", flush=True)
+
+    def bf16():
+        y = empty((M, N), np.uint16)
+        hip.gemm_small_w4a16(y, w, x, M, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def residual():
+        h = h0.clone()
+        hip.gemv_residual_w4a16(h, w, x, M, scratch)
+        _sync()
+        return host(h, np.uint16)
+
+    def swiglu():
+        y = empty((M, N // 2), np.uint16)
+        hip.gemv_swiglu_w4a16(y, w, x, M, scratch)
+        _sync()
+        return host(y, np.uint16)
+
+    def argmax():
+        idx = empty((M,), np.int32)
+        hip.gemv_argmax_w4a16(idx, w, x, M, scratch)
+        _sync()
+        return host(idx, np.int32)
+
+    for run in (bf16, residual, swiglu, argmax):
+        _staged_vs_per_item(hip, run)
+    hip.awq_free(w)
+
+
+def test_staged_rows_vs_oracle(hip, orc, scratch):
+    """One staged shape against the oracle (the GEMV bars)."""
+    N, K, M = 16384, 1024, 9
+    q, zp, s = orc.gen_weights(N, K, seed=77)
+    w = repack_from_logical(hip, orc, q, zp, s)
+    x = orc.gen_x(M, K, seed=78)
+    y = empty((M, N), np.uint16)
+    hip.gemm_small_w4a16(y, w, dev(x), M, scratch)
+    _sync()
+    m = orc.parity_metrics(host(y, np.uint16), orc.matmul_f64(x, q, zp, s))
+    print(f"staged rows vs oracle: {m}", flush=True)
+    assert m["max_rel"] <= 1e-2 and m["mean_abs_vs_bf16_ref"] <= 1e-3, m
+    hip.awq_free(w)
