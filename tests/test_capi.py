@@ -186,3 +186,20 @@ def test_host_paths_from_many_threads(hip):
         t.join()
     assert not errors, errors
     assert all(g == want for g in got), got
+
+
+def test_weights_beyond_32bit_offsets_refused(hip):
+    """The skinny kernels address packed weights through 32-bit buffer offsets:
+    a tensor of 4 GiB or more of packed words is refused before any launch
+    (QW4_ERR_SHAPE), and one just below the limit passes the size check (it
+    then fails on the scratch capacity, still before a launch)."""
+    L = hip.lib()
+    x, y = C.c_void_p(0x10000), C.c_void_p(0x20000)
+    big = _fake_weights(hip, out_f=131072, in_f=65536)            # 4 GiB of packed words
+    s = _fake_scratch(hip, tiles=131072 // 64)
+    s.max_in, s.max_out = 65536, 131072
+    assert L.qw4_gemv(y, C.byref(big), x, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    assert L.qw4_gemm_small(y, C.byref(big), x, 9, C.byref(s), None) == hip.QW4_ERR_SHAPE
+    below = _fake_weights(hip, out_f=131072 - 64, in_f=65536)
+    small = _fake_scratch(hip, tiles=1)
+    assert L.qw4_gemv(y, C.byref(below), x, C.byref(small), None) == hip.QW4_ERR_SCRATCH
