@@ -150,7 +150,10 @@ def _run(hip, orc, scratch, N, K, M, seed):
 
 
 @pytest.mark.parametrize("M", [1, 2, 9, 16])
-@pytest.mark.parametrize("N,K", [(64, 512), (5120, 5120), (31040, 5120), (640, 2176)])
+# (31040, 5120) at M = 2 and (16384, 1024) at every M > 1 run the verify kernel
+# with the activation rows staged in LDS (the default path, "dec")
+@pytest.mark.parametrize("N,K", [(64, 512), (5120, 5120), (31040, 5120), (640, 2176),
+                                 (16384, 1024)])
 def test_w8_gemv_and_verify(hip, orc, scratch, decode_path, N, K, M):
     import torch
 
