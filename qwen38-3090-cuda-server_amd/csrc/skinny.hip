@@ -601,9 +601,10 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   if (XL) {
     // x loads first, then the first weight items: waiting for x leaves the
     // weights in flight (loads complete in order). Threads past the last
-    // chunk repeat it (same address, same value), so neither the loads nor
-    // the LDS stores are conditional and the scheduler cannot sink the loads
-    // behind the weights.
+    // chunk load it again (same address), so the loads are not conditional
+    // and the scheduler cannot sink them behind the weights; only the
+    // in-range chunks are stored (a wave storing one address from every lane
+    // serializes on one LDS bank).
     const int n16 = a.M * a.K / 8;
     u32x4 xv[kXC], nv[OUT == OUT_NORM ? kXC : 1];
     int xi[kXC];
@@ -620,7 +621,8 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     __builtin_amdgcn_sched_barrier(0);
     prime();
 #pragma unroll
-    for (int j = 0; j < kXC; ++j) xlds[XM ? xi[j] + xi[j] / (a.K / 8) : xi[j]] = xv[j];
+    for (int j = 0; j < kXC; ++j)
+      if ((int)threadIdx.x + j * 64 * W < n16) xlds[XM ? xi[j] + xi[j] / (a.K / 8) : xi[j]] = xv[j];
     lds_barrier<DMA>();
     if (OUT == OUT_NORM) {
       // rmsnorm of each row in place (src/kernels/elementwise.cu:8-31):
@@ -645,6 +647,7 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
       lds_barrier<DMA>();
 #pragma unroll
       for (int j = 0; j < kXC; ++j) {
+        if ((int)threadIdx.x + j * 64 * W >= n16) continue;
         const float inv = rinv[xi[j] / kc];
         u32x4 o;
 #pragma unroll
@@ -1023,7 +1026,8 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
 #pragma unroll
     for (int j = 0; j < D; ++j) load_item(j);
 #pragma unroll
-    for (int j = 0; j < kXC; ++j) raw[xi[j]] = xv[j];
+    for (int j = 0; j < kXC; ++j)   // in-range chunks only (see k_rows's staging)
+      if ((int)threadIdx.x + j * 64 * W < n16) raw[xi[j]] = xv[j];
     lds_barrier<true>();
     __shared__ float rinv;
     if (wave == 0) {
@@ -1044,6 +1048,7 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
     const float inv = rinv;
 #pragma unroll
     for (int j = 0; j < kXC; ++j) {
+      if ((int)threadIdx.x + j * 64 * W >= n16) continue;
       u32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
