@@ -5,9 +5,9 @@
 // _residual); these stand-alone forms serve larger M and callers that keep
 // the steps apart. Data are bf16 [rows][dim]; 16-byte chunks of 8 elements.
 //
-// rmsnorm sums the squares of a row with one wave in a fixed order -- lane l
-// takes chunks l, l + 64, ..., then a butterfly -- exactly as the fused
-// qw4_gemv_rmsnorm does, so the two agree bit for bit.
+// rmsnorm sums the squares of a row in the order every form shares
+// (norm_sumsq: 1024 virtual threads, butterflies per virtual wave, the wave
+// sums in order), so it agrees with the fused qw4_gemv_rmsnorm bit for bit.
 #include <hip/hip_runtime.h>
 
 #include "../../include/qwen_w4a16.h"
@@ -22,26 +22,22 @@ __global__ __launch_bounds__(kEwThreads) void k_rmsnorm(uint16_t* __restrict__ o
                                                         const uint16_t* __restrict__ x,
                                                         const uint16_t* __restrict__ w,
                                                         int dim, float eps) {
-  const int row = blockIdx.x, lane = threadIdx.x & 63;
+  // thread t stands for the virtual threads t + 256 k of the shared order
+  // (norm_sumsq): virtual wave wave + 4 k
+  constexpr int kPer = kNormVThreads / kEwThreads;
+  const int row = blockIdx.x, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int kc = dim / 8;
   const u32x4* xr = reinterpret_cast<const u32x4*>(x + (size_t)row * dim);
-  __shared__ float inv_s;
-  if (threadIdx.x < 64) {
+  __shared__ float vsum[kNormVWaves];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
     float ss = 0.f;
-    for (int i = lane; i < kc; i += 64) {
-      const u32x4 v = xr[i];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float lo = bf16_bits_to_f32(v[e] & 0xffffu), hi = bf16_bits_to_f32(v[e] >> 16);
-        ss += lo * lo + hi * hi;
-      }
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-    if (lane == 0) inv_s = rsqrtf(ss / (float)dim + eps);
+    for (int i = threadIdx.x + kEwThreads * k; i < kc; i += kNormVThreads) ss = norm_sumsq(ss, xr[i]);
+    ss = norm_wave_sum(ss);
+    if (lane == 0) vsum[wave + (kEwThreads / 64) * k] = ss;
   }
   __syncthreads();
-  const float inv = inv_s;
+  const float inv = norm_inv(vsum, dim, eps);
   const u32x4* wr = reinterpret_cast<const u32x4*>(w);
   u32x4* orow = reinterpret_cast<u32x4*>(out + (size_t)row * dim);
   for (int i = threadIdx.x; i < kc; i += kEwThreads) {

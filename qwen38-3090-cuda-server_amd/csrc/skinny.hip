@@ -600,11 +600,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   };
   if (XL) {
     // x loads first, then the first weight items: waiting for x leaves the
-    // weights in flight (loads complete in order). Threads past the last
-    // chunk load it again (same address), so the loads are not conditional
-    // and the scheduler cannot sink them behind the weights; only the
-    // in-range chunks are stored (a wave storing one address from every lane
-    // serializes on one LDS bank).
+    // weights in flight (loads complete in order). A wave issues a round of
+    // loads only if it has chunks in range (a 16-byte load of a wave holds
+    // the CU's address unit for ~16 cycles whatever its addresses); its lanes
+    // past the last chunk load that chunk again. Only in-range chunks are
+    // stored (a wave storing one address from every lane serializes on one
+    // LDS bank).
     const int n16 = a.M * a.K / 8;
     u32x4 xv[kXC], nv[OUT == OUT_NORM ? kXC : 1];
     int xi[kXC];
@@ -613,10 +614,14 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
 #pragma unroll
     for (int j = 0; j < kXC; ++j) {
       xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
-      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
-      if (OUT == OUT_NORM)
-        nv[j & (OUT == OUT_NORM ? 0xff : 0)] = __builtin_amdgcn_raw_buffer_load_b128(
-            rn, (uint32_t)(xi[j] % (a.K / 8)) * 16u, 0, 0);
+      xv[j] = u32x4{0u, 0u, 0u, 0u};
+      nv[j & (OUT == OUT_NORM ? 0xff : 0)] = u32x4{0u, 0u, 0u, 0u};
+      if (64 * wave + j * 64 * W < n16) {   // wave-uniform: this wave has chunks in range
+        xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
+        if (OUT == OUT_NORM)
+          nv[j & (OUT == OUT_NORM ? 0xff : 0)] = __builtin_amdgcn_raw_buffer_load_b128(
+              rn, (uint32_t)(xi[j] % (a.K / 8)) * 16u, 0, 0);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     prime();
@@ -626,29 +631,28 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     lds_barrier<DMA>();
     if (OUT == OUT_NORM) {
       // rmsnorm of each row in place (src/kernels/elementwise.cu:8-31):
-      // x * rsqrt(mean(x^2) + eps) * (1 + w), fp32, rounded to bf16 once.
-      // Wave m % W sums row m's squares in a fixed order.
-      __shared__ float rinv[16];
+      // x * rsqrt(mean(x^2) + eps) * (1 + w), fp32, rounded to bf16 once; the
+      // sum of squares of row m in the shared order (norm_sumsq), thread t
+      // standing for virtual threads t + 64 W k and reading the staged row
+      constexpr int kP = kNormVThreads / (64 * W);
+      static_assert(kNormVThreads % (64 * W) == 0, "workgroup of 1024 / kP threads");
+      __shared__ float vsum[16][kNormVWaves];
       const int kc = a.K / 8;
-      for (int m = wave; m < a.M; m += W) {
-        float ss = 0.f;
-        for (int i = lane; i < kc; i += 64) {
-          const u32x4 v = xlds[m * kc + i];
+      for (int m = 0; m < a.M; ++m) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float lo = bf16_bits_to_f32(v[e] & 0xffffu), hi = bf16_bits_to_f32(v[e] >> 16);
-            ss += lo * lo + hi * hi;
-          }
+        for (int k = 0; k < kP; ++k) {
+          float ss = 0.f;
+          for (int i = (int)threadIdx.x + 64 * W * k; i < kc; i += kNormVThreads)
+            ss = norm_sumsq(ss, xlds[m * kc + i]);
+          ss = norm_wave_sum(ss);
+          if (lane == 0) vsum[m][wave + W * k] = ss;
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-        if (lane == 0) rinv[m] = rsqrtf(ss / (float)a.K + a.eps);
       }
       lds_barrier<DMA>();
 #pragma unroll
       for (int j = 0; j < kXC; ++j) {
         if ((int)threadIdx.x + j * 64 * W >= n16) continue;
-        const float inv = rinv[xi[j] / kc];
+        const float inv = norm_inv(vsum[xi[j] / kc], a.K, a.eps);
         u32x4 o;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -990,13 +994,17 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
   if constexpr (OUT != OUT_NORM) {
     // x loads of this wave's groups first (g = wave + W (4 it + lane / 16),
     // chunk lane % 16), then the first weight items; out-of-range chunks
-    // read zeros without traffic
+    // read zeros without traffic. Rounds with no group of this wave issue
+    // nothing: every 16-byte load of a wave holds the CU's address unit for
+    // ~16 cycles whatever its addresses, and 8 waves share one.
     u32x4 xv[kDecPrepIters];
 #pragma unroll
     for (int it = 0; it < kDecPrepIters; ++it) {
       const int g = wave + W * (4 * it + (lane >> 4));
-      xv[it] = __builtin_amdgcn_raw_buffer_load_b128(
-          rs.x, g < G ? (uint32_t)(g * 16 + c16) * 16u : 0x7ffffff0u, 0, 0);
+      xv[it] = u32x4{0u, 0u, 0u, 0u};
+      if (wave + W * 4 * it < G)   // wave-uniform
+        xv[it] = __builtin_amdgcn_raw_buffer_load_b128(
+            rs.x, g < G ? (uint32_t)(g * 16 + c16) * 16u : 0x7ffffff0u, 0, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1008,10 +1016,13 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
       dec_prep_chunk(xw, cst, g, c16, xv[it], g < G);
     }
   } else {
-    // rmsnorm of x (src/kernels/elementwise.cu:8-31) in the summation order
-    // of k_rmsnorm (lane l of one wave takes chunks l, l + 64, ..., then a
-    // butterfly), x * rsqrt(mean(x^2) + eps) * (1 + w) rounded to bf16 once;
-    // staged in LDS, then each wave prepares its groups from there
+    // rmsnorm of x (src/kernels/elementwise.cu:8-31) with the sum of squares
+    // in the order every rmsnorm form here shares (norm_sumsq): this thread's
+    // chunk j, t + 64 W j, belongs to virtual thread t + 64 W (j mod kP);
+    // x * rsqrt(mean(x^2) + eps) * (1 + w) rounded to bf16 once, staged in
+    // LDS, then each wave prepares its groups from there
+    constexpr int kP = kNormVThreads / (64 * W);
+    static_assert(kNormVThreads % (64 * W) == 0, "workgroup of 1024 / kP threads");
     u32x4 xv[kXC], nv[kXC];
     int xi[kXC];
     const __amdgpu_buffer_rsrc_t rn =
@@ -1019,35 +1030,31 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
 #pragma unroll
     for (int j = 0; j < kXC; ++j) {
       xi[j] = min((int)threadIdx.x + j * 64 * W, n16 - 1);
-      xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
-      nv[j] = __builtin_amdgcn_raw_buffer_load_b128(rn, (uint32_t)xi[j] * 16u, 0, 0);
+      xv[j] = nv[j] = u32x4{0u, 0u, 0u, 0u};
+      if (64 * wave + j * 64 * W < n16) {   // wave-uniform (see the loads above)
+        xv[j] = __builtin_amdgcn_raw_buffer_load_b128(rs.x, (uint32_t)xi[j] * 16u, 0, 0);
+        nv[j] = __builtin_amdgcn_raw_buffer_load_b128(rn, (uint32_t)xi[j] * 16u, 0, 0);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < D; ++j) load_item(j);
+    __shared__ float vsum[kNormVWaves];
+    float part[kP];
 #pragma unroll
-    for (int j = 0; j < kXC; ++j)   // in-range chunks only (see k_rows's staging)
-      if ((int)threadIdx.x + j * 64 * W < n16) raw[xi[j]] = xv[j];
-    lds_barrier<true>();
-    __shared__ float rinv;
-    if (wave == 0) {
-      float ss = 0.f;
-      for (int i = lane; i < n16; i += 64) {
-        const u32x4 v = raw[i];
+    for (int k = 0; k < kP; ++k) part[k] = 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float lo = bf16_bits_to_f32(v[e] & 0xffffu), hi = bf16_bits_to_f32(v[e] >> 16);
-          ss += lo * lo + hi * hi;
-        }
-      }
+    for (int j = 0; j < kXC; ++j)
+      if ((int)threadIdx.x + j * 64 * W < n16) part[j % kP] = norm_sumsq(part[j % kP], xv[j]);
 #pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off, 64);
-      if (lane == 0) rinv = rsqrtf(ss / (float)a.K + a.eps);
+    for (int k = 0; k < kP; ++k) {
+      const float sk = norm_wave_sum(part[k]);
+      if (lane == 0) vsum[wave + W * k] = sk;
     }
     lds_barrier<true>();
-    const float inv = rinv;
+    const float inv = norm_inv(vsum, a.K, a.eps);
 #pragma unroll
-    for (int j = 0; j < kXC; ++j) {
+    for (int j = 0; j < kXC; ++j) {   // in-range chunks only (see k_rows's staging)
       if ((int)threadIdx.x + j * 64 * W >= n16) continue;
       u32x4 o;
 #pragma unroll

@@ -104,6 +104,40 @@ __device__ __forceinline__ uint16_t swiglu_bf16_bits(uint32_t g, uint32_t u) {
   return to_bf16((gf / (1.f + expf(-gf))) * uf);
 }
 
+// rmsnorm's sum of squares (src/kernels/elementwise.cu:8-31 sums x^2 in
+// fp32). Every rmsnorm form here -- stand-alone and fused into the GEMVs --
+// uses this one order, so that they agree bit for bit, and it spreads over a
+// whole workgroup: 1024 virtual threads; virtual thread v adds the 16-byte
+// chunks v, v + 1024, ... of the row in order (each chunk's words in order,
+// each word as s + (lo*lo + hi*hi), every operation rounded once); each run of
+// 64 virtual threads (a virtual wave) reduces with a butterfly (xor 32, 16, 8,
+// 4, 2, 1); the 16 virtual-wave sums are added in order.
+constexpr int kNormVThreads = 1024;
+constexpr int kNormVWaves = kNormVThreads / 64;
+
+__device__ __forceinline__ float norm_sumsq(float s, const u32x4& v) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = __uint_as_float(v[e] << 16), hi = __uint_as_float(v[e] & 0xffff0000u);
+    s = __fadd_rn(s, __fadd_rn(__fmul_rn(lo, lo), __fmul_rn(hi, hi)));
+  }
+  return s;
+}
+
+__device__ __forceinline__ float norm_wave_sum(float s) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) s = __fadd_rn(s, __shfl_xor(s, off, 64));
+  return s;
+}
+
+// 1 / rms from the 16 virtual-wave sums (in LDS or registers, in order).
+__device__ __forceinline__ float norm_inv(const float* vwave, int dim, float eps) {
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormVWaves; ++i) t = __fadd_rn(t, vwave[i]);
+  return rsqrtf(t / (float)dim + eps);
+}
+
 // bf16(x * inv * (1 + w)) for bf16 x, w: the rmsnorm output rounding of the
 // reference's k_rmsnorm (src/kernels/elementwise.cu:29-30).
 __device__ __forceinline__ float rmsnorm_f32(uint32_t x, uint32_t w, float inv) {
