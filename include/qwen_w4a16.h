@@ -234,8 +234,10 @@ int qw4_gemv_swiglu(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
 /* rmsnorm then linear (model.cu:697-700, :773-777): y [M][out_f] = rmsnorm(h) @ W^T
  * with norm weight norm_w [in_f]. The normalized rows are formed in LDS and
  * never written; when they do not fit (M * in_f * 2 beyond the staging
- * limit), tmp ([M][in_f] bf16, may be NULL otherwise) receives them and the
- * plain GEMV follows. Results equal qw4_rmsnorm + qw4_gemm_small bit for bit. */
+ * limit, or at M = 1 beyond what the decode kernel stages beside its other
+ * LDS), tmp ([M][in_f] bf16, may be NULL otherwise) receives them and the
+ * plain GEMV follows; without tmp such a call returns QW4_ERR_SHAPE. Results
+ * equal qw4_rmsnorm + qw4_gemm_small bit for bit. */
 int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
                      const uint16_t* norm_w, float eps, int M, uint16_t* tmp, qw4_scratch* s,
                      void* stream);

@@ -1651,6 +1651,12 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
   const int mode = g_dec_tune.mode.load(std::memory_order_relaxed);
   if constexpr (FMT == 4) {
     DecCfg dc{};
+    // M = 1 rmsnorm that the decode kernel cannot stage (its LDS): the caller's
+    // tmp path (rmsnorm, then the decode kernel) beats the bf16 skinny kernel
+    // and equals the unfused steps
+    if (OUT == OUT_NORM && M == 1 && mode != 1 && mode != 2 && !dec_config(w.out_f, w.G, OUT, dc) &&
+        dec_config(w.out_f, w.G, OUT_BF16, dc))
+      return QW4_ERR_SHAPE;
     if (M == 1 && mode != 1 && mode != 2 && dec_config(w.out_f, w.G, OUT, dc)) {
       a.U = tiles * 4 / dc.S;
       a.P = dc.P;

@@ -84,7 +84,7 @@ def _norm_w(orc, K, seed):
 
 
 # ------------------------------------------------------ stand-alone steps
-@pytest.mark.parametrize("rows,dim", [(1, 5120), (9, 4096), (16, 17408), (3, 136)])
+@pytest.mark.parametrize("rows,dim", [(1, 5120), (9, 4096), (16, 17408), (3, 136), (2, 8704)])
 def test_rmsnorm(hip, orc, rows, dim):
     x, w = orc.gen_x(rows, dim, seed=dim + rows), _norm_w(orc, dim, 11)
     out = empty((rows, dim), np.uint16)
@@ -165,8 +165,11 @@ def test_gemv_swiglu(hip, orc, scratch, M, inter, K):
     hip.awq_free(w)
 
 
+# one group (waves without chunks), more chunks than the 1024 virtual threads
+# of the sum order (1088), and a 16-wave decode launch (K = 17408)
 @pytest.mark.parametrize("M", [1, 2, 3, 9, 16])
-@pytest.mark.parametrize("N,K", [(7168, 5120), (34816, 5120), (640, 1024)])
+@pytest.mark.parametrize("N,K", [(7168, 5120), (34816, 5120), (640, 1024), (256, 128),
+                                 (1024, 8704), (5120, 17408)])
 def test_gemv_rmsnorm(hip, orc, scratch, M, N, K):
     q, zp, s = orc.gen_weights(N, K, seed=N + M, tensor=3)
     w = repack_from_logical(hip, orc, q, zp, s)
