@@ -223,7 +223,7 @@ class Bench:
 
         # Per-projection launch duration: HIP does not allow timing events as
         # graph nodes, so each projection's 64 launches are a graph of their
-        # own, timed with events on the launch stream (includes the ~1 us gap
+        # own, timed with events on the launch stream (includes the time
         # between consecutive kernels).
         per_op, tot_ms, tot_bytes, launches = {}, 0.0, 0, 0
         for li, (name, K, N) in enumerate(LAYER):
