@@ -61,6 +61,12 @@ typedef struct qw4_weights {
 
 size_t qw4_weights_bytes(const qw4_weights* w);   /* device bytes held */
 
+/* Repacked-layout sizes (the library asserts it uses these): output rows per
+ * tile, and bytes of one (tile, group) scale record (64 bf16 scales + 16
+ * zero-point words). */
+#define QW4_TILE_ROWS 64
+#define QW4_META_BYTES 160
+
 /* awq_alloc_fused (src/kernels/gemv_w4a16.cuh:81-82; .cu:308-315). */
 int qw4_weights_alloc(qw4_weights* w, int out_f, int in_f, int group_size, void* stream);
 /* awq_free (gemv_w4a16.cuh:86; .cu:331-334). */
@@ -117,8 +123,10 @@ int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
  * every shape: see the decode design notes). */
 int qw4_choose_splits(int out_f, int num_groups);
 
-/* Tuning and test overrides (no reference counterpart; for benchmarks and
- * tests; process-wide atomics, read at each launch: set them between launches).
+/* TEST-ONLY tuning overrides: not part of the product interface (no reference
+ * counterpart). The benchmark and the tests use them to force every kernel
+ * form; a product caller never needs them and must not call them while other
+ * threads launch, since they are process-wide atomics read at each launch.
  * qw4_tune_decode, the skinny launches: mode 0 the library's measured policy;
  * 1 the bf16 skinny kernel (k_rows) instead of the integer-MFMA decode kernel
  * at M = 1, S (1, 2, 4 row quads per unit) and D (2..4) forcing its unit size
@@ -233,11 +241,14 @@ int qw4_gemv_swiglu(uint16_t* y, const qw4_weights* w, const uint16_t* x, int M,
                     qw4_scratch* s, void* stream);
 /* rmsnorm then linear (model.cu:697-700, :773-777): y [M][out_f] = rmsnorm(h) @ W^T
  * with norm weight norm_w [in_f]. The normalized rows are formed in LDS and
- * never written; when they do not fit (M * in_f * 2 beyond the staging
- * limit, or at M = 1 beyond what the decode kernel stages beside its other
- * LDS), tmp ([M][in_f] bf16, may be NULL otherwise) receives them and the
- * plain GEMV follows; without tmp such a call returns QW4_ERR_SHAPE. Results
- * equal qw4_rmsnorm + qw4_gemm_small bit for bit. */
+ * never written. When they do not fit (M > 1 with M * in_f * 2 beyond the
+ * staging limit), tmp ([M][in_f] bf16) receives them and the plain GEMV
+ * follows; without tmp such a call returns QW4_ERR_SHAPE. At M = 1 beyond what
+ * the decode kernel stages beside its other LDS, a given tmp takes the same
+ * two-step path (the faster one), and without tmp the bf16 skinny kernel
+ * normalizes the row in LDS itself (within the GEMV tolerance of the two-step
+ * result, not bitwise equal to it). Otherwise results equal qw4_rmsnorm +
+ * qw4_gemm_small bit for bit. tmp may be NULL. */
 int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
                      const uint16_t* norm_w, float eps, int M, uint16_t* tmp, qw4_scratch* s,
                      void* stream);

@@ -39,8 +39,10 @@ struct W4A16Weights {
   int out_f = 0, in_f = 0, group_size = 0, num_groups = 0;
 
   size_t qweight_bytes() const { return size_t(out_f) * in_f / 2; }
-  // per (64-row tile, group) one 160-byte record: 64 bf16 scales + 16 zero words
-  size_t scale_bytes() const { return size_t(out_f) / 64 * num_groups * 160; }
+  // per (64-row tile, group) one record: 64 bf16 scales + 16 zero-point words
+  size_t scale_bytes() const {
+    return size_t(out_f) / QW4_TILE_ROWS * num_groups * QW4_META_BYTES;
+  }
   size_t zp_bytes() const { return size_t(out_f) * num_groups / 2; }
   size_t total_bytes() const { return qweight_bytes() + scale_bytes() + zp_bytes(); }
 };

@@ -92,8 +92,10 @@ __device__ __forceinline__ uint64_t argmax_key(float v, int n) {
   return ((uint64_t)u << 32) | (uint64_t)(~(uint32_t)n);
 }
 
-__device__ __forceinline__ uint32_t inc_dev(uint32_t* p) {
-  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Arrival: release this workgroup's key updates, and acquire those of the
+// workgroups counted before it (the last arriver then reads every key).
+__device__ __forceinline__ uint32_t arrive_dev(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void clear_dev(uint32_t* p) {
   __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -210,7 +212,10 @@ __device__ __forceinline__ void argmax_arrive(const SkinnyArgs& a, int p, Best& 
     const uint32_t in_grp = (uint32_t)((a.P - 1 - grp) / kKeyGroups + 1);
     uint32_t* gcnt = a.counters + (size_t)grp * kCounterStride;
     uint32_t* done = a.counters + (size_t)kKeyGroups * kCounterStride;
-    if (inc_dev(gcnt) == in_grp - 1 && inc_dev(done) == (uint32_t)(ngroups - 1)) {
+    // memory order: each workgroup's key updates happen before its release
+    // increment of its group counter; the group's last arriver acquires them
+    // and releases them on `done`, whose last arriver acquires all of them
+    if (arrive_dev(gcnt) == in_grp - 1 && arrive_dev(done) == (uint32_t)(ngroups - 1)) {
       int32_t* idx = static_cast<int32_t*>(a.y);
       for (int m = 0; m < a.M; ++m) {
         uint64_t best = 0;
@@ -840,9 +845,14 @@ __device__ __forceinline__ void dec_prep_chunk(uint32_t* xw, u32x4* cst, int g, 
   m = row16_max(m);   // |x| bits of the group's largest element
   // 2^sh scales it into [2^20, 2^21): 1.5 * 2^23 + 0x8080 + X stays in
   // [2^23, 2^24), where the fp32 ulp is 1
+  // A group holding Inf or NaN (exponent 255) gets a NaN constant, so every
+  // output is NaN, as the reference's fp32 group sum gives (Inf - Inf). A group
+  // whose largest |x| is an fp32 subnormal (below 2^-126) keeps the cap 2^126:
+  // its terms then round to ~0, an absolute error below 2^-100 per output.
   const int sh = min(20 - ((int)(m >> 23) - 127), 126);
   const float p2 = __uint_as_float((uint32_t)(sh + 127) << 23);
-  const float inv = __uint_as_float((uint32_t)(127 - sh) << 23);
+  const float inv = (m >> 23) >= 255u ? __uint_as_float(0x7fc00000u)
+                                      : __uint_as_float((uint32_t)(127 - sh) << 23);
   // T = X + 0x8080: byte 0 = c + 128, byte 1 = b + 128, byte 2 = a
   uint32_t t[8];
 #pragma unroll
@@ -1614,7 +1624,14 @@ struct Epi {
   const uint16_t* res = nullptr;
   const uint16_t* nw = nullptr;
   float eps = 0.f;
+  bool tmp_ok = false;   // OUT_NORM: the caller can run rmsnorm into a buffer first
 };
+
+// run_skinny's internal status (never returned through the C-ABI): an rmsnorm
+// projection to run as rmsnorm into the caller's buffer, then the plain
+// projection -- rows beyond the LDS staging, or an M = 1 row the decode kernel
+// cannot stage (where that path is the faster one).
+constexpr int kStatusNeedTmp = -100;
 
 template <int OUT, int FMT>
 int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scratch* s,
@@ -1654,9 +1671,9 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
     // M = 1 rmsnorm that the decode kernel cannot stage (its LDS): the caller's
     // tmp path (rmsnorm, then the decode kernel) beats the bf16 skinny kernel
     // and equals the unfused steps
-    if (OUT == OUT_NORM && M == 1 && mode != 1 && mode != 2 && !dec_config(w.out_f, w.G, OUT, dc) &&
-        dec_config(w.out_f, w.G, OUT_BF16, dc))
-      return QW4_ERR_SHAPE;
+    if (OUT == OUT_NORM && M == 1 && e.tmp_ok && mode != 1 && mode != 2 &&
+        !dec_config(w.out_f, w.G, OUT, dc) && dec_config(w.out_f, w.G, OUT_BF16, dc))
+      return kStatusNeedTmp;
     if (M == 1 && mode != 1 && mode != 2 && dec_config(w.out_f, w.G, OUT, dc)) {
       a.U = tiles * 4 / dc.S;
       a.P = dc.P;
@@ -1666,7 +1683,8 @@ int run_skinny(void* y, const WeightView& w, const uint16_t* x, int M, qw4_scrat
     }
   }
   const Launch l = launch_for<OUT, FMT>(w.out_f, w.G, M);
-  if (OUT == OUT_NORM && !l.XL) return QW4_ERR_SHAPE;   // x must fit the LDS staging
+  // x must fit the LDS staging; beyond it, the caller's tmp path or an error
+  if (OUT == OUT_NORM && !l.XL) return e.tmp_ok ? kStatusNeedTmp : QW4_ERR_SHAPE;
   a.P = l.P;
   a.U = tiles * 4 / l.S;
   launch_rows<OUT, FMT>(a, l, (hipStream_t)stream);
@@ -1711,11 +1729,6 @@ int run_skinny8(void* y, const qw4_w8_weights* w, const uint16_t* x, int M, qw4_
 constexpr int kNoAllocKeyWords = kKeyGroups * 16;
 constexpr int kNoAllocWords = kNoAllocKeyWords + (kKeyGroups + 1) * kCounterStride / 2;
 
-__global__ void k_zero_u64(uint64_t* p, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) p[i] = 0;
-}
-
 }  // namespace
 }  // namespace qw4
 
@@ -1724,40 +1737,35 @@ static __device__ __align__(256) uint64_t scratch[qw4::kNoAllocWords];
 namespace qw4 {
 namespace {
 
-// Set-up once per device (with that device current): the array's address,
-// kept per device, and one zero fill on the caller's stream (a kernel, so a
-// first call under graph capture records it; every later call relies on the
-// argmax's own reset of keys and counters at its end).
+// Per-device address of `scratch`, looked up once with that device current.
+// The array is zero when the code object loads and every call's last
+// workgroup clears what it used, so no set-up kernel runs (a first call under
+// graph capture records nothing extra). A failed look-up is not cached: the
+// next call tries again.
 struct NoAllocState {
-  std::once_flag once;
-  uint64_t* ptr = nullptr;
-  int status = QW4_ERR_HIP;
+  std::mutex mu;
+  std::atomic<uint64_t*> ptr{nullptr};
 };
 NoAllocState g_noalloc[kMaxDevices];
 
-int noalloc_scratch(uint64_t*& ptr, hipStream_t stream) {
+int noalloc_scratch(uint64_t*& ptr) {
   NoAllocState& st = g_noalloc[current_device()];
-  std::call_once(st.once, [&st, stream] {
-    void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess || !p) {
-      set_hip_error((int)e);
-      (void)hipGetLastError();
-      return;
-    }
-    prepare_dma_lds();
-    k_zero_u64<<<(kNoAllocWords + 255) / 256, 256, 0, stream>>>(static_cast<uint64_t*>(p),
-                                                                kNoAllocWords);
-    const hipError_t e2 = hipGetLastError();
-    if (e2 != hipSuccess) {
-      set_hip_error((int)e2);
-      return;
-    }
-    st.ptr = static_cast<uint64_t*>(p);
-    st.status = QW4_OK;
-  });
-  ptr = st.ptr;
-  return st.status;
+  ptr = st.ptr.load(std::memory_order_acquire);
+  if (ptr) return QW4_OK;
+  std::lock_guard<std::mutex> lock(st.mu);
+  ptr = st.ptr.load(std::memory_order_relaxed);
+  if (ptr) return QW4_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p) {
+    set_hip_error((int)e);
+    (void)hipGetLastError();
+    return QW4_ERR_HIP;
+  }
+  prepare_dma_lds();
+  ptr = static_cast<uint64_t*>(p);
+  st.ptr.store(ptr, std::memory_order_release);
+  return QW4_OK;
 }
 
 }  // namespace
@@ -1863,7 +1871,7 @@ int qw4_gemv_argmax_noalloc(int32_t* idx, const qw4_weights* w, const uint16_t* 
                             void* stream) {
   if (M < 1 || M > 16) return QW4_ERR_M;   // the keys hold 16 rows
   uint64_t* p = nullptr;
-  const int st = noalloc_scratch(p, (hipStream_t)stream);
+  const int st = noalloc_scratch(p);
   if (st) return st;
   qw4_scratch s{};
   s.keys = p;
@@ -1903,10 +1911,12 @@ int qw4_gemv_rmsnorm(uint16_t* y, const qw4_weights* w, const uint16_t* h,
   Epi e;
   e.nw = norm_w;
   e.eps = eps;
+  e.tmp_ok = tmp != nullptr;
   const int st = run_skinny<OUT_NORM>(y, w, h, M, s, stream, e);
-  if (st != QW4_ERR_SHAPE || !tmp) return st;
-  // activations too large to stage: rmsnorm into tmp, then the plain GEMV
-  if (!w || !h) return QW4_ERR_NULL;
+  if (st != kStatusNeedTmp) return st;
+  // M = 1 activations the decode kernel cannot stage: rmsnorm into tmp, then
+  // the decode kernel (without tmp the call runs the bf16 skinny kernel, which
+  // stages them)
   const int st2 = qw4_rmsnorm(tmp, h, norm_w, M, w->in_f, eps, stream);
   if (st2) return st2;
   return run_skinny<OUT_BF16>(y, w, tmp, M, s, stream);

@@ -30,6 +30,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "../../include/qwen_w4a16.h"
+
 namespace qw4 {
 
 constexpr int kTileN = 64;          // output rows per tile
@@ -37,6 +39,8 @@ constexpr int kGroup = 128;         // inputs per quantization group
 constexpr int kWordsPerBlock = 1024;  // u32 words per (tile, group)
 constexpr int kMetaU16 = 80;        // u16 per (tile, group) in the 4-bit scale array
 constexpr int kMetaBytes = 2 * kMetaU16;
+static_assert(kTileN == QW4_TILE_ROWS && kMetaBytes == QW4_META_BYTES,
+              "the public layout sizes in qwen_w4a16.h");
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));

@@ -61,6 +61,16 @@ int main() {
   qwen::W4A16Weights W;
   qwen::awq_repack(W, d_packed, reinterpret_cast<__hip_bfloat16*>(d_scale), d_zp, N, K, 128);
   CK(hipDeviceSynchronize());
+  {   // the C++ size helpers agree with the library's allocation
+    qw4_weights cw{W.qweight, reinterpret_cast<uint16_t*>(W.scale),
+                   reinterpret_cast<uint16_t*>(W.zp), W.out_f, W.in_f, W.group_size,
+                   W.num_groups};
+    if (W.total_bytes() != qw4_weights_bytes(&cw)) {
+      std::printf("FAIL total_bytes %zu vs qw4_weights_bytes %zu\n", W.total_bytes(),
+                  qw4_weights_bytes(&cw));
+      return 1;
+    }
+  }
   // the reference frees its sources right after the repack (model.cu:124-125)
   CK(hipFree(d_packed));
   CK(hipFree(d_scale));

@@ -190,6 +190,23 @@ def test_gemv_rmsnorm(hip, orc, scratch, M, N, K):
     hip.awq_free(w)
 
 
+def test_gemv_rmsnorm_m1_without_tmp(hip, orc, scratch):
+    """M = 1 at K = 17408: beyond the decode kernel's staging, so with tmp the
+    call runs rmsnorm + decode GEMV (bitwise the unfused steps, checked in
+    test_gemv_rmsnorm); without tmp it runs the bf16 skinny kernel with the row
+    normalized in LDS, held to the GEMV bars against the oracle composition."""
+    N, K, M = 5120, 17408, 1
+    q, zp, s = orc.gen_weights(N, K, seed=2, tensor=6)
+    w = repack_from_logical(hip, orc, q, zp, s)
+    h, nw = orc.gen_x(M, K, seed=9), _norm_w(orc, K, 4)
+    y = empty((M, N), np.uint16)
+    hip.gemv_rmsnorm_w4a16(y, w, dev(h), dev(nw), EPS, M, scratch)
+    _sync()
+    xr = orc.rmsnorm_bf16(h, nw, EPS)
+    _check(orc, host(y, np.uint16), orc.matmul_f64(xr, q, zp, s), "gemv_rmsnorm M=1 no tmp")
+    hip.awq_free(w)
+
+
 def test_gemv_rmsnorm_needs_tmp_when_not_staged(hip, orc, scratch):
     """M = 16 rows of K = 5120 do not fit the LDS staging: without tmp the call
     reports a shape error instead of computing something else."""
