@@ -315,11 +315,29 @@ struct DmaSlot {
   static constexpr int kUnits = kNQ * 64 + 16 + (FMT == 4 ? 16 : 0);
 };
 
+// k_rows item slot with LDS-DMA items (16-byte units): DmaSlot's weights and
+// metadata, then -- when the activations are not staged for the whole
+// workgroup (!XL: M > 1 rows of a long K) -- the item's group of all 16
+// activation rows (rows past M read as zeros), 16 chunks per row, chunk j of
+// row r at unit 16 r + (j ^ r): the 16 lanes reading one k-chunk of rows
+// 0..15 hit 16 different 16-byte bank groups.
+template <int FMT, int S, bool XL>
+constexpr int rows_slot_units() {
+  return DmaSlot<FMT, S>::kUnits + (XL ? 0 : 256);
+}
+
 // 16 bytes per lane, nontemporal (weights); 4 bytes per lane (metadata)
 __device__ __forceinline__ void dma_load16(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff,
                                            uint32_t soff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
                                            voff, soff, 0, kWeightAux);
+}
+// 16 bytes per lane, default cache policy (activations: every workgroup
+// reads them, mostly from L2)
+__device__ __forceinline__ void dma_load16c(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff,
+                                            uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, soff, 0, 0);
 }
 __device__ __forceinline__ void dma_load4(__amdgpu_buffer_rsrc_t r, u32x4* dst, uint32_t voff,
                                           uint32_t soff) {
@@ -524,7 +542,9 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   constexpr uint32_t kPer = 4 / S;   // units per tile (unit indices are never negative)
   constexpr uint32_t kQuad = FMT == 8 ? 512u : 256u;
   constexpr int kRedLanes = kM1 ? 16 : 64;
-  constexpr int kRedBufs = XM ? 1 : 2;   // XM: one buffer (LDS), a second barrier per unit
+  // XM, and 8-bit items with their activations in the slots: one buffer (LDS),
+  // a second barrier per unit
+  constexpr int kRedBufs = (XM || (DMA && !XL && FMT == 8)) ? 1 : 2;
   constexpr int kXC = XM ? kRowsXmChunks : rows_xchunks(DMA);
   __shared__ f32x4 red[kRedBufs][W][S][kRedLanes];
   extern __shared__ u32x4 xlds[];
@@ -571,21 +591,30 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
 
   RowsData<FMT, S, XL> buf[kM1 ? 1 : D];
   const int xs16 = a.K / 8 + (XM ? 1 : 0);   // staged row stride, 16-byte chunks
-  u32x4* const ring = xlds + (XL ? a.M * xs16 : 0) + wave * D * DmaSlot<FMT, S>::kUnits;
+  constexpr int kSlotU = rows_slot_units<FMT, S, XL>();
+  u32x4* const ring = xlds + (XL ? a.M * xs16 : 0) + wave * D * kSlotU;
+  // !XL: lane l of activation load t fetches row 4 t + l / 16, chunk
+  // (l % 16) ^ row, into slot unit 64 t + l (see rows_slot_units)
+  const int xr_ = lane >> 4, xj_ = lane & 15;
+  uint32_t xdoff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    xdoff[t] = (uint32_t)(4 * t + xr_) * (uint32_t)a.K * 2u +
+               (uint32_t)((xj_ ^ (4 * t + xr_)) & 15) * 16u;
   auto load_slot = [&](int j) __attribute__((always_inline)) {
     const bool in = lu < u1;
     const int ru = real_unit(lu);
     const int b = in ? (int)((uint32_t)ru / kPer) : 0;
     const int st0 = in ? (int)((uint32_t)ru % kPer) * S : 0;
     const int g = in ? lg : 0;
-    dma_issue<FMT, S>(ring + j * DmaSlot<FMT, S>::kUnits, rs,
+    dma_issue<FMT, S>(ring + j * kSlotU, rs,
                       in ? (uint32_t)b * (uint32_t)a.G + (uint32_t)g : oob_blk,
                       wbase + (uint32_t)st0 * kQuad, lane);
     if (!XL) {
+      u32x4* const xs = ring + j * kSlotU + DmaSlot<FMT, S>::kUnits;
 #pragma unroll
       for (int t = 0; t < 4; ++t)
-        buf[j & (kM1 ? 0 : 0xff)].x[t & (XL ? 0 : 3)] =
-            __builtin_amdgcn_raw_buffer_load_b128(rs.x, xoff + t * 16, (uint32_t)g * 256u, 0);
+        dma_load16c(rs.x, xs + 64 * t, xdoff[t], (uint32_t)g * 256u);
     }
     lg += W;
     if (lg >= a.G) {
@@ -739,10 +768,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
       wait_vm<decltype(nc)::value>();
       const int st0 = (int)((uint32_t)real_unit(closed) % kPer) * S;
       RowsData<FMT, S, XL> d;
-      dma_read<FMT, S, XL>(d, ring + j * DmaSlot<FMT, S>::kUnits, lane, st0);
+      dma_read<FMT, S, XL>(d, ring + j * kSlotU, lane, st0);
       if constexpr (!XL) {
+        // row c, k-chunk 4 q + t (the k order of the register form, xoff)
+        const u32x4* xs = ring + j * kSlotU + DmaSlot<FMT, S>::kUnits + 16 * c;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) d.x[t & (XL ? 0 : 3)] = buf[j & (kM1 ? 0 : 0xff)].x[t & (XL ? 0 : 3)];
+        for (int t = 0; t < 4; ++t) d.x[t & (XL ? 0 : 3)] = xs[(4 * q + t) ^ c];
       }
       rows_mma<FMT, S, XL, kM1 ? 1 : 4>(acc, d, k, st0, zsh, xrow + cg * 16);
       if (reload) {
@@ -1373,11 +1404,20 @@ Launch launch_for(int out_f, int G, int M) {
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, (long long)cus));
       return l;
     }
-    const int S = l.S;
+    int S = l.S;
     const int dd = (mode == 1 && tD >= 2 && tD <= 4 && !(OUT == OUT_ARGMAX && S == 4)) ? tD : 2;
-    const int slot = (FMT == 8 ? 2 * S : S) * 1024 + (FMT == 4 ? 512 : 256);
-    const int need = 8 * dd * slot + 2 * 8 * S * 64 * 16;
+    // weights, metadata and the item's 16 activation rows (rows_slot_units)
+    auto need_for = [&](int s_) {
+      const int slot = (FMT == 8 ? 2 * s_ : s_) * 1024 + (FMT == 4 ? 512 : 256) + 4096;
+      return 8 * dd * slot + (FMT == 8 ? 1 : 2) * 8 * s_ * 64 * 16;
+    };
+    // 64-row units whose slots do not fit: 32-row units with the activations
+    // in the slots (measured on MI355X: gate|up at M = 16, 28.1 us against 29.6
+    // for 64-row units with the activations loaded into registers)
+    if (S == 4 && need_for(4) > kLdsBytes && !(mode == 1 && tS == 4)) S = 2;
+    const int need = need_for(S);
     if (need <= kLdsBytes) {
+      l.S = S;
       l.DMA = dd;
       l.W = 8;
       l.XL = false;
@@ -1514,7 +1554,7 @@ void prepare_dec() {
 
 template <int OUT, int FMT, int S, int W, int D, bool XL, bool XM = false>
 void launch_rows_dma_d(const SkinnyArgs& a, hipStream_t st) {
-  const int lds = (XL ? a.M * (a.K * 2 + (XM ? 16 : 0)) : 0) + W * D * DmaSlot<FMT, S>::kUnits * 16;
+  const int lds = (XL ? a.M * (a.K * 2 + (XM ? 16 : 0)) : 0) + W * D * rows_slot_units<FMT, S, XL>() * 16;
   constexpr auto kern = &k_rows<OUT, FMT, S, W, XL, D, true, XM>;
   allow_lds<kern>(lds);
   kern<<<a.P, 64 * W, lds, st>>>(a);
