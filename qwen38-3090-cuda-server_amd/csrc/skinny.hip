@@ -371,6 +371,17 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
+// Wait until at most n items' loads (kL each) of this wave are outstanding,
+// n in [0, D) known only at run time (the immediate needs a switch).
+template <int kL, int D>
+__device__ __forceinline__ void wait_items(int n) {
+  static_for<0, D>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if (n == i) wait_vm<i * kL>();
+  });
+}
+
+
 template <int FMT, int S>
 __device__ __forceinline__ void dma_issue(u32x4* slot, const SkinnyRsrc& r, uint32_t blk,
                                           uint32_t woff, int lane) {
@@ -763,9 +774,12 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
     // item t waits for its slot; the loads of the items after it (all D - 1
     // of them in the main loop, fewer in the tail) may still be in flight
     constexpr int kL = DmaSlot<FMT, S>::kLoads + (XL ? 0 : 4);
-    auto step_dma = [&](auto jc, auto nc, bool reload) __attribute__((always_inline)) {
+    auto step_dma = [&](auto jc, auto nc, bool reload, int nwait = 0) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value;
-      wait_vm<decltype(nc)::value>();
+      if constexpr (decltype(nc)::value >= 0)
+        wait_vm<decltype(nc)::value>();
+      else
+        wait_items<kL, D>(nwait);
       const int st0 = (int)((uint32_t)real_unit(closed) % kPer) * S;
       RowsData<FMT, S, XL> d;
       dma_read<FMT, S, XL>(d, ring + j * kSlotU, lane, st0);
@@ -787,13 +801,20 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
         close_unit();
       }
     };
-    for (; t0 + D <= T; t0 += D)
+    // whole batches whose reloads are all real items, then the last r < 2 D
+    // items: item j reloads only a real item (j + D < r) and waits for the
+    // min(D - 1, r - 1 - j) items loaded after it (no load is issued past
+    // the last item: an out-of-range LDS-DMA load costs as much as a real one)
+    for (; t0 + 2 * D <= T; t0 += D)
       static_for<0, D>([&](auto jc) {
         step_dma(jc, std::integral_constant<int, (D - 1) * kL>{}, true);
       });
-    static_for<0, D - 1>([&](auto jc) {
+    const int r = T - t0;
+    static_for<0, 2 * D - 1>([&](auto jc) {
       constexpr int j = decltype(jc)::value;
-      if (t0 + j < T) step_dma(jc, std::integral_constant<int, (D - 1 - j) * kL>{}, false);
+      if (j < r)
+        step_dma(std::integral_constant<int, j % D>{}, std::integral_constant<int, -1>{},
+                 j + D < r, min(D - 1, r - 1 - j));
     });
   } else {
     for (; t0 + D <= T; t0 += D) {
@@ -1168,10 +1189,13 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
   constexpr int kL = S + 1;   // loads per item
   // item j waits for its slot (the loads of the D - 1 items after it may
   // still be in flight)
-  auto step = [&](auto jc, auto nc, bool reload) __attribute__((always_inline)) {
+  auto step = [&](auto jc, auto nc, bool reload, int nwait = 0) __attribute__((always_inline)) {
     constexpr int j = decltype(jc)::value;
     const int st0 = (int)((uint32_t)real_unit(cu) % kPer) * S;
-    wait_vm<decltype(nc)::value>();
+    if constexpr (decltype(nc)::value >= 0)
+      wait_vm<decltype(nc)::value>();
+    else
+      wait_items<kL, D>(nwait);
     RowsData<4, S, true> d;
     dec_read<S>(d, ring + j * kDecSlot<S>, lane, st0);
     dec_mma<S>(acc, d, xq + cg * kDecQ, cst[cg], aoff, st0, zsh);
@@ -1186,11 +1210,15 @@ __global__ __launch_bounds__(64 * W) void k_dec(SkinnyArgs a) {
       ++cu;
     }
   };
-  for (; t0 + D <= T; t0 += D)
+  // whole batches, then the last r < 2 D items with no load past the end (as k_rows)
+  for (; t0 + 2 * D <= T; t0 += D)
     static_for<0, D>([&](auto jc) { step(jc, std::integral_constant<int, (D - 1) * kL>{}, true); });
-  static_for<0, D - 1>([&](auto jc) {
+  const int r = T - t0;
+  static_for<0, 2 * D - 1>([&](auto jc) {
     constexpr int j = decltype(jc)::value;
-    if (t0 + j < T) step(jc, std::integral_constant<int, (D - 1 - j) * kL>{}, false);
+    if (j < r)
+      step(std::integral_constant<int, j % D>{}, std::integral_constant<int, -1>{}, j + D < r,
+           min(D - 1, r - 1 - j));
   });
   while (cu < u1) {   // waves with no items (wave >= G)
     close_unit(cu);
