@@ -1442,7 +1442,9 @@ Launch launch_for(int out_f, int G, int M) {
     // 64-row units whose slots do not fit: 32-row units with the activations
     // in the slots (measured on MI355X: gate|up at M = 16, 28.1 us against 29.6
     // for 64-row units with the activations loaded into registers)
-    if (S == 4 && need_for(4) > kLdsBytes && !(mode == 1 && tS == 4)) S = 2;
+    // (4-bit only: the 8-bit head at M = 9 keeps its 64-row register form,
+    // 352 against 368 us for 32-row units with the activations in the slots)
+    if (FMT == 4 && S == 4 && need_for(4) > kLdsBytes && !(mode == 1 && tS == 4)) S = 2;
     const int need = need_for(S);
     if (need <= kLdsBytes) {
       l.S = S;
