@@ -119,8 +119,10 @@ int qw4_scratch_free(qw4_scratch* s);
 int qw4_partial_check(const qw4_scratch* s, int splits, int out_f, int M);
 /* gemv_choose_splits (gemv_w4a16.cuh:134; .cu:289-306): cross-workgroup
  * K-splits the skinny kernels use for this shape. Always 1: every workgroup
- * owns whole output rows over all of K (measured on MI355X, splitting lost at
- * every shape: see the decode design notes). */
+ * owns whole output rows over all of K. On MI355X every K split measured
+ * (partials exchanged between workgroups as tagged agent-scope words, or
+ * summed by a second kernel as the reference does) was slower than whole
+ * rows at the decode and verify shapes. */
 int qw4_choose_splits(int out_f, int num_groups);
 
 /* TEST-ONLY tuning overrides: not part of the product interface (no reference
