@@ -534,7 +534,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the W4A16 path is single-GPU; "
-              "multi-GPU sharding is a design note, not a measured mode). Use --gpus 1.",
+              "multi-GPU sharding is described, not measured). Use --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
 

@@ -358,7 +358,7 @@ def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
 
 # ------------------------------------------------------------ checkpoints
 def test_checkpoint_fused_load(hip, orc, scratch, tmp_path):
-    """SURVEY next-row 1: a compressed-tensors checkpoint (weight_packed I32
+    """A compressed-tensors checkpoint (weight_packed I32
     [N][K/8], weight_scale BF16 [N][G], weight_zero_point I32 [N/8][G], the
     reference's on-disk format) read by the library's safetensors reader and
     fused like the reference's fuse() (model.cu:103-128): q, k and v of one
