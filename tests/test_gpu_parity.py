@@ -196,6 +196,33 @@ def test_verify_config3_shapes(hip, orc, scratch, N, K):
     hip.awq_free(w)
 
 
+def test_verify_every_m(hip, orc, scratch):
+    """Every verify row count M = 2..16 on one shape (the activation rows past
+    M in each item's slot read as zeros; the unit sums cover rows 4q + jj < M),
+    against the oracle, and each row bitwise equal to the same row computed
+    with M = 16 (rows are independent in the kernel)."""
+    import torch
+
+    N, K = 5120, 4096
+    q, zp, s = orc.gen_weights(N, K, seed=77)
+    w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
+    x16 = orc.gen_x(16, K, seed=78)
+    y16 = empty((16, N), np.uint16)
+    hip.gemm_small_w4a16(y16, w, dev(x16), 16, scratch)
+    torch.cuda.synchronize()
+    full = host(y16, np.uint16).reshape(16, N)
+    ref = orc.matmul_f64(x16, q, zp, s)
+    _check_bf16(orc, full, ref, "verify M=16")
+    for M in range(2, 16):
+        y = empty((M, N), np.uint16)
+        hip.gemm_small_w4a16(y, w, dev(np.ascontiguousarray(x16[:M])), M, scratch)
+        torch.cuda.synchronize()
+        got = host(y, np.uint16).reshape(M, N)
+        _check_bf16(orc, got, ref[:M], f"verify M={M}")
+        assert np.array_equal(got, full[:M]), M
+    hip.awq_free(w)
+
+
 def test_mma_entry_matches_small(hip, orc, scratch):
     import torch
 
