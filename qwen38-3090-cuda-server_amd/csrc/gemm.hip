@@ -308,43 +308,73 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
   }
 }
 
-// D: lane holds column m = 32 mb + r and rows 8 jq + 4 h + i, i.e. output
-// columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
+// Tile store. Accumulator layout: lane holds column m = 32 mb + r and rows
+// 8 jq + 4 h + i, i.e. output columns n = 64 tile + 4 (8 b + 2 jq + h) + i.
+// Stored from that layout directly, a store instruction writes 8 bytes per
+// lane to 32 rows (16-byte pieces of 32 lines), and the partial-line requests
+// bound the store of a tile (gate M = 4096: ~10% of the kernel's time). So the
+// tile goes through LDS and every store instruction writes whole 128-byte row
+// segments of C: each wave stages its own region of the 128 KiB activation
+// buffers (its rows x NH * 64 bytes, 16-byte chunk c of row m at c ^ (m %
+// CPR)) -- after a wait and a barrier, so that all waves are done with the
+// segment's operand reads and their loads have landed -- and reads it back
+// row by row. Measured: gate M = 4096 0.617 -> 0.601 ms.
 template <int NH, int NW>
-__device__ __forceinline__ void g2_store(const GemmArgs& a,
-                                         const f32x16v (&acc)[NH][G2Split<NH, NW>::MBW], int m0,
-                                         int tile, int b0, int mw, int lane) {
+__device__ __forceinline__ void g2_store_staged(const GemmArgs& a,
+                                                const f32x16v (&acc)[NH][G2Split<NH, NW>::MBW],
+                                                u32x4* lds, int m0, int tile, int b0, int mw,
+                                                bool valid, int wave, int lane) {
   constexpr int MBW = G2Split<NH, NW>::MBW;
+  constexpr int CPR = NH * 4;                      // 16-byte chunks per staged row
+  constexpr int ROWS = MBW * 32;
+  constexpr int RPI = 64 / CPR;                    // rows per read-back instruction
   const int r = lane & 31, h = lane >> 5;
+  g2_wait_vm0();
+  __syncthreads();
+  u32x4* reg = lds + wave * (ROWS * CPR);
+  uint32_t* reg32 = reinterpret_cast<uint32_t*>(reg);
 #pragma unroll
   for (int mb = 0; mb < MBW; ++mb) {
-    const int m = m0 + 32 * (mw + mb) + r;
-    if (m >= a.M) continue;
-    uint16_t* crow = a.C + (size_t)m * a.N + tile * kTileN;
+    const int row = 32 * mb + r;
 #pragma unroll
     for (int j = 0; j < NH; ++j)
 #pragma unroll
       for (int jq = 0; jq < 4; ++jq) {
+        const int c = (4 * j + jq) ^ (row % CPR);
         const u32x2 o = {pack_bf16x2(acc[j][mb][4 * jq], acc[j][mb][4 * jq + 1]),
                          pack_bf16x2(acc[j][mb][4 * jq + 2], acc[j][mb][4 * jq + 3])};
-        *reinterpret_cast<u32x2*>(crow + 4 * (8 * (b0 + j) + 2 * jq + h)) = o;
+        *reinterpret_cast<u32x2*>(reg32 + (row * CPR + c) * 4 + 2 * h) = o;
       }
+  }
+  __builtin_amdgcn_wave_barrier();
+  asm volatile("" ::: "memory");
+  if (!valid) return;
+  const int cl = lane % CPR;
+#pragma unroll
+  for (int t = 0; t < ROWS / RPI; ++t) {
+    const int row = RPI * t + lane / CPR;
+    const u32x4 v = reg[row * CPR + (cl ^ (row % CPR))];
+    const int m = m0 + 32 * mw + row;
+    if (m < a.M)
+      *reinterpret_cast<u32x4*>(a.C + (size_t)m * a.N + tile * kTileN + 32 * b0 + 8 * cl) = v;
   }
 }
 
 // Stream-K partial tiles. Each workgroup has two fp32 slots (for its first
-// and its last tile), laid out [wave][m-block][lane] in 64-byte runs. A
-// workgroup whose range cuts a tile writes its partial there; a second kernel
-// (k_gemm_fixup, stream-ordered after this one) sums each cut tile's slots in
-// workgroup order -- a fixed order, so results are bitwise reproducible -- and
-// stores the tile.
+// and its last tile), laid out [wave][pair][i][lane]: 16-byte piece i of a
+// lane's 64 bytes at 1024 i + 16 lane, so that every store (and the fixup's
+// every load) covers 1 KiB contiguously; lane-major 64-byte runs made each
+// instruction write 16-byte pieces of 32 lines (down M = 512: 0.111 -> 0.098
+// ms). A workgroup whose range cuts a tile writes its partial there; a second
+// kernel (k_gemm_fixup, stream-ordered after this one) sums each cut tile's
+// slots in workgroup order -- a fixed order, so results are bitwise
+// reproducible -- and stores the tile.
 constexpr uint32_t kSlotBytes = (uint32_t)G2_BM * G2_BN * 4;   // 256 KiB
 
 // idx: the wave's (half, m-block) pair j * MBW + mb, of `units` per wave.
 __device__ __forceinline__ uint32_t g2_slot_off(int vp, int which, int wave, int units, int idx,
                                                 int lane) {
-  return (uint32_t)(vp * 2 + which) * kSlotBytes +
-         (uint32_t)(((wave * units + idx) * 64 + lane) * 64);
+  return (uint32_t)(vp * 2 + which) * kSlotBytes + (uint32_t)((wave * units + idx) * 4096 + lane * 16);
 }
 
 template <int NH, int NW>
@@ -362,7 +392,7 @@ __device__ __forceinline__ void g2_slot_store(__amdgpu_buffer_rsrc_t rs,
         const u32x4 v = {__float_as_uint(acc[j][mb][4 * i]), __float_as_uint(acc[j][mb][4 * i + 1]),
                          __float_as_uint(acc[j][mb][4 * i + 2]),
                          __float_as_uint(acc[j][mb][4 * i + 3])};
-        __builtin_amdgcn_raw_buffer_store_b128(v, rs, off + 16 * i, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, off + 1024 * i, 0, 0);
       }
     }
 }
@@ -427,7 +457,7 @@ __global__ __launch_bounds__(64) void k_gemm_fixup(GemmArgs a) {
             live ? g2_slot_off(q, which, wave, Sp::UNITS, part * kPer + e, lane) : 0x80000000u;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          v[k][e][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 16 * i, 0, 0);
+          v[k][e][i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off + 1024 * i, 0, 0);
       }
     }
 #pragma unroll
@@ -493,7 +523,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
     const bool valid = tile * kTileN < a.N;
     const int ltile = valid ? tile : (a.N / kTileN - 1);
     g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, 0, a.G, wave, lane);
-    if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+    g2_store_staged<NH, NW>(a, acc, &lds[0][0], tm * G2_BM, tile, b0, mw, valid, wave, lane);
   }
   for (int u = u0; u < u1;) {
     const int ts = u / a.G, g0 = u - ts * a.G;
@@ -505,7 +535,7 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
     const int ltile = valid ? tile : (a.N / kTileN - 1);
     g2_segment<NH, NW>(a, wr, lds, acc, tm * G2_BM, ltile, b0, mw, g0, g1, wave, lane);
     if (g0 == 0 && g1 == a.G) {
-      if (valid) g2_store<NH, NW>(a, acc, tm * G2_BM, tile, b0, mw, lane);
+      g2_store_staged<NH, NW>(a, acc, &lds[0][0], tm * G2_BM, tile, b0, mw, valid, wave, lane);
     } else {
       g2_slot_store<NH, NW>(rs, acc, vp, u == u0 ? 0 : 1, wave, lane);
     }
