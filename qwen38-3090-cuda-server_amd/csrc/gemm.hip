@@ -492,7 +492,10 @@ template <int NH, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
   using Sp = G2Split<NH, NW>;
   constexpr int MBW = Sp::MBW;              // m-blocks per wave
-  __shared__ u32x4 lds[2][G2_BM * 16];      // 2 x 64 KiB: [row][16 swizzled chunks]
+  // 2 x 64 KiB: [row][16 swizzled chunks]. The kernel's only LDS variable, so
+  // it starts at LDS offset 0: with a 16-byte word placed before it the
+  // kernel ran ~40% slower (the LDS-DMA and operand-read patterns assume it).
+  __shared__ u32x4 lds[2][G2_BM * 16];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int lane = threadIdx.x & 63;
   int wt, b0, mw;
@@ -632,8 +635,9 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     //  * hybrid: whole tiles for the floor(nt / CUs) full rounds, then the
     //    other nt % CUs tiles split over the CUs: the same work, one partial
     //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile.
-    // A split schedule runs when it beats per-tile by 10% (qw4_tune_gemm
-    // forces one, for tests and tuning).
+    // A split schedule runs when it beats per-tile by 5% (qw4_tune_gemm
+    // forces one, for tests and tuning): gate M = 512, 136 tiles, costs 37.6
+    // against 40 and measured 0.880 against 0.842 PFLOP/s.
     const int sk_env = g_gemm_schedule.load(std::memory_order_relaxed);
     const int cus = device_cus();
     const long long G = w->num_groups;
@@ -650,7 +654,7 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     if (sk_env == 1 && sk_ok) pick = 1;
     else if (sk_env == 2 && hy_ok) pick = 2;
     else if (sk_env == -1) {
-      double best = 0.9 * t_dp;
+      double best = 0.95 * t_dp;
       if (sk_ok && t_sk < best) { pick = 1; best = t_sk; }
       if (hy_ok && t_hy < best) pick = 2;
     }
