@@ -492,10 +492,7 @@ template <int NH, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
   using Sp = G2Split<NH, NW>;
   constexpr int MBW = Sp::MBW;              // m-blocks per wave
-  // 2 x 64 KiB: [row][16 swizzled chunks]. The kernel's only LDS variable, so
-  // it starts at LDS offset 0: with a 16-byte word placed before it the
-  // kernel ran ~40% slower (the LDS-DMA and operand-read patterns assume it).
-  __shared__ u32x4 lds[2][G2_BM * 16];
+  __shared__ u32x4 lds[2][G2_BM * 16];      // 2 x 64 KiB: [row][16 swizzled chunks]
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
   const int lane = threadIdx.x & 63;
   int wt, b0, mw;
