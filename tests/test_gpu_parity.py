@@ -352,6 +352,32 @@ def test_prefill_kernel_variants_bitwise(hip, orc, gemm_ws, M, N, K):
     hip.awq_free(w)
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 5120, 2176), (77, 320, 1024), (1100, 17408, 5120)])
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_prefill_c_8_byte_aligned(hip, orc, gemm_ws, M, N, K, use_ws):
+    """C needs only 8-byte alignment (the header's rule): the tile stores
+    write 16-byte row segments, which must land the same at an address 8
+    bytes past a 16-byte boundary. Bitwise equal to the aligned call, and
+    nothing written outside C."""
+    import torch
+
+    q, zp, s = orc.gen_weights(N, K, seed=M + 5)
+    x = orc.gen_x(M, K, seed=M + 5)
+    w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
+    dx = dev(x)
+    ws = gemm_ws if use_ws else None
+    y = empty((M, N), np.uint16)
+    hip.gemm_w4a16(y, w, dx, M, ws)
+    big = torch.full((M * N + 8,), 0x5A5A, dtype=torch.int16, device="cuda")
+    y8 = big[4:4 + M * N].view(M, N)
+    assert y8.data_ptr() % 16 == 8
+    hip.gemm_w4a16(y8, w, dx, M, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(y8, y)
+    assert (big[:4] == 0x5A5A).all() and (big[4 + M * N:] == 0x5A5A).all()
+    hip.awq_free(w)
+
+
 @pytest.mark.parametrize("M,N,K", [(4096, 17408, 5120), (4096, 5120, 17408), (1024, 17408, 5120),
                                    (1024, 5120, 17408)])
 def test_prefill_gemm_full_vs_torch_fp32(hip, orc, gemm_ws, M, N, K):
