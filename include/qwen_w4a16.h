@@ -140,7 +140,8 @@ int qw4_choose_splits(int out_f, int num_groups);
  * workgroup count. */
 int qw4_tune_decode(int mode, int S, int W, int D, int P);
 /* qw4_tune_gemm: the prefill schedule, -1 the cost model (default), 0 one
- * workgroup per tile, 1 stream-K, 2 hybrid (split schedules need a workspace);
+ * workgroup per tile, 1 stream-K, 2 hybrid, 3 split-K (every tile cut into the
+ * same k-slices; at most CUs / 2 tiles) (split schedules need a workspace);
  * variant 0 the default kernel (4 waves, each on a whole 64-row weight tile
  * against all 256 activation rows), 1 8 waves on 32-row tile halves, 2 8 waves
  * on whole tiles against 128 rows; the variants' results are bitwise equal. */

@@ -64,6 +64,8 @@ struct GemmArgs {
   float* slots;         // stream-K: [P][2] fp32 partial tiles
   int M, N, K, G, tiles_n, tiles_m, map;
   int P;                // workgroups
+  // map: 0 blockIdx order; 1 XCD-contiguous runs of workgroups; 2 split-K:
+  // XCD-contiguous runs over (k-slice, tile row-major), P / tiles slices
   int full;             // tiles [0, full) are done whole, P at a time
   int U;                // (tile, group) units of tiles [full, tiles), split over P
 };
@@ -182,6 +184,11 @@ __device__ __forceinline__ void g2_wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F7
 // share an activation tile (and, 4 apart, a weight tile), so the ~32
 // workgroups an XCD runs at once touch ~4 activation and ~8 weight tiles.
 __device__ __forceinline__ void g2_tile_coords(const GemmArgs& a, int t, int& tn, int& tm) {
+  if (a.map == 2) {   // split-K: row-major, so an XCD's run shares the rows of A
+    tm = t / a.tiles_n;
+    tn = t - tm * a.tiles_n;
+    return;
+  }
   const int band = 4 * a.tiles_n;
   const int b = t / band, w = t % band;
   const int rows = min(4, a.tiles_m - 4 * b);
@@ -504,7 +511,16 @@ __global__ __launch_bounds__(64 * NW, 1) void k_gemm(GemmArgs a) {
   // start(vp + 1)) of the U = (tiles - full) x G units of the remaining
   // tiles: ranges that cut a tile (stream-K) are combined through slots.
   // P = tiles, full = tiles: one whole tile per workgroup.
-  const int vp = a.map ? g2_xcd_order(blockIdx.x, a.P) : (int)blockIdx.x;
+  int vp = a.map ? g2_xcd_order(blockIdx.x, a.P) : (int)blockIdx.x;
+  if (a.map == 2) {
+    // Split-K: the P = tiles x S ranges are the S k-slices of each tile (vp =
+    // tile S + slice). The XCD runs go over slices, then tiles row-major, so
+    // the ~30 workgroups of an XCD work on the same k-slice of one or two
+    // rows of tiles: they share A's rows in their L2, at the same k.
+    const int nt = a.tiles_n * a.tiles_m, S = a.P / nt;
+    const int sl = vp / nt, ts = vp - sl * nt;
+    vp = ts * S + sl;
+  }
   const int u0 = g2_range_start(a, vp), u1 = g2_range_start(a, vp + 1);
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(a.slots, 0, (int)(2u * a.P * kSlotBytes), 0x00020000);
@@ -561,7 +577,7 @@ int device_cus() {
 }
 
 // Tuning and test override of the prefill schedule (qw4_tune_gemm): -1 the
-// cost model, 0 per tile, 1 stream-K, 2 hybrid.
+// cost model, 0 per tile, 1 stream-K, 2 hybrid, 3 split-K.
 std::atomic<int> g_gemm_schedule{-1};
 // Kernel variant (qw4_tune_gemm): 0 the default, 4 waves of whole 64-row
 // tiles against all 256 activation rows; 1 8 waves of 32-row tile halves; 2 8
@@ -599,7 +615,7 @@ int qw4_workspace_free(qw4_workspace* ws) {
 }
 
 int qw4_tune_gemm(int schedule, int variant) {
-  if (schedule < -1 || schedule > 2 || variant < 0 || variant > 2) return QW4_ERR_SHAPE;
+  if (schedule < -1 || schedule > 3 || variant < 0 || variant > 2) return QW4_ERR_SHAPE;
   g_gemm_schedule.store(schedule, std::memory_order_relaxed);
   g_gemm_variant.store(variant, std::memory_order_relaxed);
   return QW4_OK;
@@ -631,7 +647,13 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
     //    a tile's pieces one after another);
     //  * hybrid: whole tiles for the floor(nt / CUs) full rounds, then the
     //    other nt % CUs tiles split over the CUs: the same work, one partial
-    //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile.
+    //    per workgroup (+8), CUs / (nt % CUs) pieces per cut tile;
+    //  * split-K (at most CUs / 2 tiles): every tile cut into the same S
+    //    k-slices, S = CUs / nt (P = nt S workgroups, a multiple of 8, at
+    //    least 2 groups per slice): G / S + 8 + 0.1 S. Against stream-K it
+    //    writes one partial per workgroup instead of up to two, and the
+    //    workgroups of an XCD share A at the same k (down M = 1024: 0.159
+    //    against 0.170-0.180 ms; down M = 512 0.094 against 0.102-0.107).
     // A split schedule runs when it beats per-tile by 5% (qw4_tune_gemm
     // forces one, for tests and tuning): gate M = 512, 136 tiles, costs 37.6
     // against 40 and measured 0.880 against 0.842 PFLOP/s.
@@ -647,15 +669,28 @@ int qw4_gemm(uint16_t* C, const qw4_weights* w, const uint16_t* A, int M, qw4_wo
                        rem != 0 && (long long)nt * G < (1LL << 31);
     const bool sk_ok = ws_ok && (long long)nt * G >= 2LL * cus;
     const bool hy_ok = ws_ok && nt > cus && (long long)rem * G >= (long long)cus;
-    int pick = 0;   // 0 per tile, 1 stream-K, 2 hybrid
+    int S = 2 * nt <= cus ? (int)std::min<long long>(cus / nt, G / 2) : 0;
+    while (S >= 2 && (nt * S) % 8) --S;
+    const bool kk_ok = ws_ok && S >= 2;
+    const double t_kk = (double)G / (S > 0 ? S : 1) + 8.0 + 0.1 * S;
+    int pick = 0;   // 0 per tile, 1 stream-K, 2 hybrid, 3 split-K
     if (sk_env == 1 && sk_ok) pick = 1;
     else if (sk_env == 2 && hy_ok) pick = 2;
+    else if (sk_env == 3 && kk_ok) pick = 3;
     else if (sk_env == -1) {
       double best = 0.95 * t_dp;
       if (sk_ok && t_sk < best) { pick = 1; best = t_sk; }
-      if (hy_ok && t_hy < best) pick = 2;
+      if (hy_ok && t_hy < best) { pick = 2; best = t_hy; }
+      if (kk_ok && t_kk < best) pick = 3;
     }
-    if (pick) {
+    if (pick == 3) {
+      a.slots = static_cast<float*>(ws->buf);
+      a.P = nt * S;
+      a.full = 0;
+      a.U = (int)(nt * G);
+      a.map = 2;
+      grid = a.P;
+    } else if (pick) {
       a.slots = static_cast<float*>(ws->buf);
       a.P = cus;
       a.full = pick == 2 ? nt - rem : 0;

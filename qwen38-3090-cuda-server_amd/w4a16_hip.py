@@ -426,7 +426,7 @@ def tune_decode(mode: int = 0, S: int = 0, W: int = 0, D: int = 0, P: int = 0) -
 
 def tune_gemm(schedule: int = -1, variant: int = 0) -> None:
     """Prefill override (qw4_tune_gemm): schedule -1 cost model, 0 per tile,
-    1 stream-K, 2 hybrid; variant 0 the default 4-wave kernel, 1 8 waves on
+    1 stream-K, 2 hybrid, 3 split-K; variant 0 the default 4-wave kernel, 1 8 waves on
     32-row tile halves, 2 8 waves on whole tiles (bitwise-equal results)."""
     _chk(lib().qw4_tune_gemm(schedule, variant), "tune_gemm")
 

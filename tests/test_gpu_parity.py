@@ -328,8 +328,8 @@ def test_prefill_kernel_variants_bitwise(hip, orc, gemm_ws, M, N, K):
     """The three prefill kernels (the default 4 waves of whole 64-row tiles, 8
     waves of tile halves, 8 waves of whole tiles against half the rows) sum
     every output in the same order: under each schedule (per tile, stream-K,
-    hybrid) their results are bitwise equal. The default is checked against
-    the oracle above."""
+    hybrid, split-K) their results are bitwise equal. The default is checked
+    against the oracle above."""
     import torch
 
     q, zp, s = orc.gen_weights(N, K, seed=M + 5)
@@ -337,7 +337,7 @@ def test_prefill_kernel_variants_bitwise(hip, orc, gemm_ws, M, N, K):
     w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
     dx = dev(x)
     try:
-        for sched in (0, 1, 2):
+        for sched in (0, 1, 2, 3):
             outs = []
             for variant in (0, 1, 2):
                 hip.tune_gemm(sched, variant)
@@ -347,6 +347,37 @@ def test_prefill_kernel_variants_bitwise(hip, orc, gemm_ws, M, N, K):
             torch.cuda.synchronize()
             for variant in (1, 2):
                 assert torch.equal(outs[0], outs[variant]), f"schedule {sched} variant {variant}"
+    finally:
+        hip.tune_gemm(-1, 0)
+    hip.awq_free(w)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 5120, 17408), (1024, 5120, 4096), (300, 5120, 2176),
+                                   (77, 320, 1024), (200, 896, 5120)])
+def test_prefill_every_schedule_vs_oracle(hip, orc, gemm_ws, M, N, K):
+    """Each schedule forced in turn (per tile, stream-K, hybrid, split-K; one
+    that does not apply to the shape falls back to per tile): sampled rows
+    against the oracle, and each schedule reproducible bitwise on a second
+    call. Split-K cuts every tile at the same k-slices; its fp32 partials are
+    summed in slice order by the fixup kernel."""
+    import torch
+
+    q, zp, s = orc.gen_weights(N, K, seed=M + 9)
+    x = orc.gen_x(M, K, seed=M + 9)
+    w = repack_from_logical(hip, orc, q, zp, s, "awq_k")
+    dx = dev(x)
+    rows = np.unique(np.r_[0, M - 1, np.random.default_rng(M).integers(0, M, 14)])
+    ref = orc.matmul_f64(x[rows], q, zp, s, round_w=True)
+    try:
+        for sched in (0, 1, 2, 3):
+            hip.tune_gemm(sched, 0)
+            y = empty((M, N), np.uint16)
+            hip.gemm_w4a16(y, w, dx, M, gemm_ws)
+            y1 = empty((M, N), np.uint16)
+            hip.gemm_w4a16(y1, w, dx, M, gemm_ws)
+            torch.cuda.synchronize()
+            assert torch.equal(y, y1), f"schedule {sched} not reproducible"
+            _check_bf16(orc, host(y, np.uint16)[rows], ref, f"prefill {M}x{N}x{K} schedule {sched}")
     finally:
         hip.tune_gemm(-1, 0)
     hip.awq_free(w)
