@@ -6,8 +6,9 @@
 // registers to exactly RNE((q - z) * s) -- the reference's k_dequant_rows
 // arithmetic (gemm_w4a16.cu:26-36) -- and feeds them to bf16 MFMA against
 // activation tiles staged in LDS. Tiles that would leave CUs idle in a last
-// partial round are instead split across workgroups (stream-K) when a
-// workspace is given; the workspace then holds fp32 partial tiles.
+// partial round are instead split across workgroups (stream-K, hybrid or
+// split-K) when a workspace is given; the workspace then holds fp32 partial
+// tiles, summed in a fixed order by a second kernel.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -48,8 +49,8 @@ namespace {
 //    row -- and reads the activation chunk 8 s + 4 h + t, the same k.
 //  * Row permutation: MFMA row r of tile half b reads tile position
 //    p = 16 (r % 4) + 8 b + 2 (r / 8) + (r / 4) % 2, so the four D rows a lane
-//    holds for each r / 8 are four consecutive output columns: one 8-byte
-//    store.
+//    holds for each r / 8 are four consecutive output columns (an 8-byte
+//    piece of a staged row, see g2_store_staged).
 constexpr int G2_BM = 256, G2_BN = 256;
 constexpr int G2_ROWBLOCKS = G2_BM / 4;  // 1 KiB (4-row) activation loads per group
 
@@ -415,9 +416,9 @@ __device__ __forceinline__ int g2_owner_of(const GemmArgs& a, int u) {
 
 // The cut tiles' fp32 partials are summed by many small blocks: block
 // (tile ts, main-kernel wave w, part) owns the pairs [part * 2, part * 2 + 2)
-// of wave w's region (the slot layout [wave][pair][lane] keeps them
+// of wave w's region (the slot layout [wave][pair][i][lane] keeps them
 // contiguous), so a cut tile is read by 32 blocks at once instead of one
-// workgroup. A block loads kFixAhead pieces before it adds them, in piece
+// workgroup (one workgroup summing its tile inside k_gemm measured slower). A block loads kFixAhead pieces before it adds them, in piece
 // order, so that the loads of a tile split many ways overlap instead of
 // paying one memory latency per piece. Tiles a single workgroup covered were
 // stored by the main kernel.
