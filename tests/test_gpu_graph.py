@@ -4,7 +4,7 @@ kernels to be capturable: no sync, no allocation, self-resetting scratch).
 
 One hipGraph holds a decode GEMV (LDS-DMA items), a verify GEMM (M = 9), both
 argmax heads, the fused residual / swiglu / rmsnorm steps, the W8 GEMV and a
-prefill GEMM whose tiles are split (stream-K partials + fixup). It is replayed
+prefill GEMM whose tiles are split (split-K partials + fixup). It is replayed
 several times with eager work and synchronisations between the replays; every
 replay must equal the eager results bitwise (the split counters, argmax keys
 and fixed-point words reset themselves, and the summation order is fixed)."""
@@ -65,7 +65,7 @@ def test_graph_replays_match_eager(hip):
     del src
     x5, x9 = _x(hip, 5120, 6), _x(hip, 9 * 5120, 7)
     x17 = _x(hip, 17408, 8)
-    a_pf = _x(hip, 512 * 17408, 9)     # down M=512: every tile split
+    a_pf = _x(hip, 512 * 17408, 9)     # down M=512: every tile split (split-K, 6 k-slices)
     h0 = _x(hip, 5120, 10)
     nw = torch.zeros(5120, dtype=torch.int16, device="cuda")
     outs = {
