@@ -188,9 +188,10 @@ int qw4_gemv_argmax_noalloc(int32_t* idx, const qw4_weights* w, const uint16_t* 
  * GemmWorkspace (src/kernels/gemm_w4a16.cuh:30-35). The fused kernel needs no
  * dequantized-weight buffer; a workspace of at least 2 x CUs x 256 KiB
  * (128 MiB on MI355X; the reference allocates 256 MiB, model.cu:440) lets it
- * split tiles across workgroups (stream-K) when whole tiles would leave CUs
- * idle. The workspace then holds fp32 partial tiles: calls that share one must
- * be stream-ordered. NULL or smaller: one workgroup per tile. */
+ * split tiles across workgroups (stream-K, hybrid, or split-K when there are
+ * at most CUs / 2 tiles) when whole tiles would leave CUs idle. The workspace
+ * then holds fp32 partial tiles: calls that share one must be stream-ordered.
+ * NULL or smaller: one workgroup per tile. */
 typedef struct qw4_workspace {
   void* buf;
   size_t bytes;
