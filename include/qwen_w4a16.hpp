@@ -19,7 +19,7 @@
 //     public fields max_m and partial_elems keep their meaning.
 //   * GemmWorkspace holds no BLAS handle and no dequantized weights: the prefill
 //     GEMM is one fused kernel; a workspace of >= 2 x CUs x 256 KiB lets it
-//     split tiles across workgroups (stream-K partials live there).
+//     split tiles across workgroups (their fp32 partials live there).
 //   * group_size must be 128; out_f % 64 == 0 and in_f % 128 == 0.
 #pragma once
 #include <hip/hip_bf16.h>
