@@ -304,15 +304,18 @@ __device__ __forceinline__ void rows_load(RowsData<FMT, S, XL>& d, const SkinnyR
 // bounded by LDS, not by registers. The compiler does not order LDS reads
 // after these loads: each item waits with an explicit vmcnt (the loads issued
 // after it, which complete after it) before reading its slot.
-// Slot layout (16-byte units): NQ x 64 weight chunks, then 256 bytes of scales
-// (lane l: the scale word l & 31 of the 64-row block), then 256 bytes of zero
-// points (lane l: word l & 7; 4-bit formats only).
+// Slot layout (16-byte units): NQ x 64 weight chunks, then a 256-byte area
+// for the block's metadata, one 4-byte load per lane: 4-bit, the 160-byte
+// (scale, zero-point) record (lane l < 40: word l; the others repeat word 0);
+// 8-bit, the 128 bytes of scales (lane l: word l & 31). One metadata load per
+// item instead of a scale and a zero-point load: every LDS-DMA instruction
+// holds the CU's address unit ~16 cycles whatever its size.
 template <int FMT, int S>
 struct DmaSlot {
   static constexpr int kH = FMT == 8 ? 2 : 1;          // 16-byte chunks per row quad
   static constexpr int kNQ = S * kH;                     // weight loads per item
-  static constexpr int kLoads = kNQ + 1 + (FMT == 4);    // loads per item
-  static constexpr int kUnits = kNQ * 64 + 16 + (FMT == 4 ? 16 : 0);
+  static constexpr int kLoads = kNQ + 1;                 // loads per item
+  static constexpr int kUnits = kNQ * 64 + 16;
 };
 
 // k_rows item slot with LDS-DMA items (16-byte units): DmaSlot's weights and
@@ -393,9 +396,11 @@ __device__ __forceinline__ void dma_issue(u32x4* slot, const SkinnyRsrc& r, uint
 #pragma unroll
     for (int h = 0; h < L::kH; ++h)
       dma_load16(r.qw, slot + (i * L::kH + h) * 64, woff + i * kQuad + h * 16, blk * kBlk);
-  dma_load4(r.sc, slot + L::kNQ * 64, (uint32_t)(lane & 31) * 4u,
-            blk * (FMT == 8 ? 128u : (uint32_t)kMetaBytes));
-  if (FMT == 4) dma_load4(r.zr, slot + L::kNQ * 64 + 16, (uint32_t)(lane & 7) * 4u, blk * 32u);
+  if (FMT == 4)
+    dma_load4(r.sc, slot + L::kNQ * 64, lane < 40 ? (uint32_t)lane * 4u : 0u,
+              blk * (uint32_t)kMetaBytes);
+  else
+    dma_load4(r.sc, slot + L::kNQ * 64, (uint32_t)(lane & 31) * 4u, blk * 128u);
 }
 
 template <int FMT, int S, bool XL>
@@ -414,7 +419,7 @@ __device__ __forceinline__ void dma_read(RowsData<FMT, S, XL>& d, const u32x4* s
   } else {
     d.s[0] = sm[(4 * c + st0) >> 1];
   }
-  if (FMT == 4) d.z = reinterpret_cast<const uint32_t*>(slot + L::kNQ * 64 + 16)[c >> 1];
+  if (FMT == 4) d.z = sm[32 + (c >> 1)];   // the record's copy of the zero-point words
 }
 
 // XL: activations come from LDS (xl: this lane's row, k chunk q, group g);
@@ -1400,7 +1405,7 @@ Launch launch_for(int out_f, int G, int M) {
     const int dd = (mode == 1 && tD >= 2 && tD <= 4) ? tD
                    : (OUT == OUT_NORM || FMT == 8)    ? 0
                                                       : (2 * tiles >= 3 * cus ? 4 : (G >= 64 ? 3 : 2));
-    const int slot = (FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256);
+    const int slot = (FMT == 8 ? 4 : 2) * 1024 + 256;
     const int need = xbytes + 8 * dd * slot + 2 * 8 * 2 * 16 * 16 + (OUT == OUT_NORM ? 64 : 0);
     if (dd >= 2 && xbytes <= rows_xchunks(true) * 16 * 64 * 8 && need <= kLdsBytes) {
       l.DMA = dd;
@@ -1419,7 +1424,7 @@ Launch launch_for(int out_f, int G, int M) {
     // units per workgroup) 22.3 against 24.1 us; with one unit per workgroup
     // (qkv, o_proj) within +-5% either way, so those keep the per-item loads.
     const int xm_need = M * (G * kGroup * 2 + 16) +
-                        8 * 2 * ((FMT == 8 ? 4 : 2) * 1024 + (FMT == 4 ? 512 : 256)) +
+                        8 * 2 * ((FMT == 8 ? 4 : 2) * 1024 + 256) +
                         8 * 2 * 64 * 16 + 512;
     if (mode != 1 && mode != 4 && 2LL * tiles > cus && M * G * kGroup / 8 <= kRowsXmChunks * 64 * 8 &&
         xm_need <= kLdsBytes) {
@@ -1436,7 +1441,7 @@ Launch launch_for(int out_f, int G, int M) {
     const int dd = (mode == 1 && tD >= 2 && tD <= 4 && !(OUT == OUT_ARGMAX && S == 4)) ? tD : 2;
     // weights, metadata and the item's 16 activation rows (rows_slot_units)
     auto need_for = [&](int s_) {
-      const int slot = (FMT == 8 ? 2 * s_ : s_) * 1024 + (FMT == 4 ? 512 : 256) + 4096;
+      const int slot = (FMT == 8 ? 2 * s_ : s_) * 1024 + 256 + 4096;
       return 8 * dd * slot + (FMT == 8 ? 1 : 2) * 8 * s_ * 64 * 16;
     };
     // 64-row units whose slots do not fit: 32-row units with the activations
