@@ -136,8 +136,9 @@ int qw4_choose_splits(int out_f, int num_groups);
  * registers for every M, S (1, 2, 4 row quads per unit) and W (8, 16 waves)
  * forcing its shape; 3 the decode kernel with unit size S, W waves and D items
  * per wave (0 = the policy's value); 4 the policy with the M > 1 activations
- * never staged in LDS (loaded with each item). P > 0 forces the decode kernel's
- * workgroup count. */
+ * never staged in LDS and never shared by a workgroup's units (loaded with
+ * each item); 5 the policy without the group-major M > 1 kernel. P > 0 forces
+ * the decode kernel's workgroup count. */
 int qw4_tune_decode(int mode, int S, int W, int D, int P);
 /* qw4_tune_gemm: the prefill schedule, -1 the cost model (default), 0 one
  * workgroup per tile, 1 stream-K, 2 hybrid, 3 split-K (every tile cut into the

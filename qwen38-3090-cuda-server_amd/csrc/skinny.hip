@@ -837,6 +837,159 @@ __global__ __launch_bounds__(64 * W) void k_rows(SkinnyArgs a) {
   if constexpr (DMA) wait_vm<0>();
 }
 
+// ------------------------------------- verify, several units per workgroup
+// k_rows_gm: M > 1, 4-bit weights, 32-row units, 8 waves, for shapes where
+// every workgroup owns n units, kGmMinU <= n <= kGmMaxU (gate|up: 4 or 5).
+// k_rows loads an item's group of the 16 activation rows with every item, so
+// a workgroup fetches each activation group n times; here the items run
+// group-major -- wave w takes groups g = w + W gi and, for each, first loads
+// the group's activation rows once into one of two activation slots (four
+// 1 KiB LDS-DMA loads), then the n weight items (u0 + ui, g) into a ring of
+// kGmD weight slots -- so the activations are fetched once per workgroup and
+// group. Each wave keeps the n units' sums and the units are summed over the
+// waves at the end. Math per item and the unit sums' order are k_rows's, so
+// the results are bitwise equal to k_rows with LDS-DMA items.
+// Slot reuse: the activation slot of group gi + 2 is loaded with the first
+// item of that group, kGmD items before it is consumed, when every item of
+// group gi (n >= kGmD of them) has been consumed.
+constexpr int kGmD = 3;      // weight items in flight per wave
+constexpr int kGmMinU = 3;   // = kGmD: the activation slots' reuse rule
+constexpr int kGmMaxU = 6;   // unit sums kept per wave
+
+// s_waitcnt vmcnt(n) for a wave-uniform n in [0, 15].
+__device__ __forceinline__ void wait_vm_rt(int n) {
+  static_for<0, 16>([&](auto ic) {
+    constexpr int i = decltype(ic)::value;
+    if (n == i) wait_vm<i>();
+  });
+}
+
+__host__ __device__ constexpr int gm_wave_units() {
+  return kGmD * DmaSlot<4, 2>::kUnits + 2 * 256;
+}
+
+template <int OUT>
+__global__ __launch_bounds__(512) void k_rows_gm(SkinnyArgs a) {
+  constexpr int FMT = 4, S = 2, W = 8, D = kGmD;
+  constexpr uint32_t kPer = 4 / S;
+  constexpr uint32_t kQuad = 256u;
+  constexpr int kWU = DmaSlot<FMT, S>::kUnits;
+  constexpr int kLw = DmaSlot<FMT, S>::kLoads;   // loads of a weight item
+  constexpr int kLx = 4;                         // loads of an activation group
+  static_assert(kLw + kLx + kLw <= 15, "wait range");
+  __shared__ f32x4 red[2][W][S][64];
+  extern __shared__ u32x4 gm_lds[];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int c = lane & 15, q = lane >> 4;
+  const SkinnyRsrc rs = skinny_rsrc(a);
+  const int zsh = 16 * (c & 1);
+  const uint32_t wbase = Fmt<FMT>::woff(q, c);
+  const int p = blockIdx.x;
+  const int u0 = range_start(a, p), n = range_start(a, p + 1) - u0;   // kGmMinU..kGmMaxU
+  const NibConst k = nib_const();
+  Best bs;
+  best_init(bs);
+  u32x4* const wring = gm_lds + wave * gm_wave_units();
+  u32x4* const xring = wring + D * kWU;
+  const int xr_ = lane >> 4, xj_ = lane & 15;
+  uint32_t xdoff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t)
+    xdoff[t] = (uint32_t)(4 * t + xr_) * (uint32_t)a.K * 2u +
+               (uint32_t)((xj_ ^ (4 * t + xr_)) & 15) * 16u;
+
+  const int ng = wave < a.G ? (a.G - 1 - wave) / W + 1 : 0;   // groups of this wave
+  const int T = ng * n;                                        // items of this wave
+  // load cursor (wave-uniform): group index lgi, unit index lui
+  int lgi = 0, lui = 0;
+  // issue the next item into weight slot j; returns its load count
+  auto issue = [&](int j) __attribute__((always_inline)) -> int {
+    const int g = wave + W * lgi;
+    int nl = kLw;
+    if (lui == 0) {   // the group's first item: its activation rows first
+      u32x4* const xs = xring + (lgi & 1) * 256;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) dma_load16c(rs.x, xs + 64 * t, xdoff[t], (uint32_t)g * 256u);
+      nl += kLx;
+    }
+    const int u = u0 + lui;
+    const int st0 = (int)((uint32_t)u % kPer) * S;
+    dma_issue<FMT, S>(wring + j * kWU, rs, (uint32_t)((uint32_t)u / kPer) * (uint32_t)a.G + (uint32_t)g,
+                      wbase + (uint32_t)st0 * kQuad, lane);
+    if (++lui == n) {
+      lui = 0;
+      ++lgi;
+    }
+    return nl;
+  };
+  // load counts of the items in flight after the one being consumed (FIFO)
+  int f1 = 0, f2 = 0;
+  static_assert(D == 3, "FIFO of two");
+  int li = 0;   // items issued
+  const int np = T < D ? T : D;
+  int f0 = 0;
+  if (np > 0) f0 = issue(0);
+  if (np > 1) f1 = issue(1);
+  if (np > 2) f2 = issue(2);
+  li = np;
+
+  f32x4 acc[kGmMaxU][S];
+#pragma unroll
+  for (int ui = 0; ui < kGmMaxU; ++ui)
+#pragma unroll
+    for (int i = 0; i < S; ++i) acc[ui][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  int j = 0;   // weight slot of the item being consumed
+  for (int gi = 0; gi < ng; ++gi) {
+    const u32x4* const xs = xring + (gi & 1) * 256 + 16 * c;
+    static_for<0, kGmMaxU>([&](auto uc) {
+      constexpr int ui = decltype(uc)::value;
+      if (ui < n) {
+        wait_vm_rt(f1 + f2);   // this item's loads (and its group's rows) have landed
+        const int u = u0 + ui;
+        const int st0 = (int)((uint32_t)u % kPer) * S;
+        RowsData<FMT, S, false> d;
+        dma_read<FMT, S, false>(d, wring + j * kWU, lane, st0);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d.x[t] = xs[(4 * q + t) ^ c];
+        rows_mma<FMT, S, false>(acc[ui], d, k, st0, zsh, nullptr);
+        // the slot's LDS reads have returned before it is loaded again
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        int fn = 0;
+        if (li < T) {
+          fn = issue(j);
+          ++li;
+        }
+        f0 = f1;
+        f1 = f2;
+        f2 = fn;
+        j = j + 1 == D ? 0 : j + 1;
+      }
+    });
+  }
+  (void)f0;
+  // unit sums over the waves, in wave order (k_rows's close_unit)
+  static_for<0, kGmMaxU>([&](auto uc) {
+    constexpr int ui = decltype(uc)::value;
+    if (ui < n) {
+#pragma unroll
+      for (int i = 0; i < S; ++i) red[ui & 1][wave][i][lane] = acc[ui][i];
+      lds_barrier<true>();
+      if (wave == 0) {
+        f32x4 t[S];
+#pragma unroll
+        for (int i = 0; i < S; ++i) t[i] = red[ui & 1][0][i][lane];
+        for (int w = 1; w < W; ++w)
+#pragma unroll
+          for (int i = 0; i < S; ++i) t[i] += red[ui & 1][w][i][lane];
+        const int u = u0 + ui;
+        emit_rows<OUT, S>(a, (int)((uint32_t)u / kPer), (int)((uint32_t)u % kPer) * S, t, lane, bs);
+      }
+    }
+  });
+  wait_vm<0>();   // no load lands in LDS after the workgroup released it
+}
+
 // ------------------------------------------------- decode with integer MFMA
 // k_dec: M = 1, 4-bit weights. The work split and epilogues are k_rows's
 // (whole units per workgroup, waves split K, unit sums in LDS in wave order);
@@ -1277,6 +1430,7 @@ struct Launch {
   bool XL;       // activations staged in LDS
   int DMA = 0;   // items in LDS slots, this many per wave (0: registers)
   bool XM = false;   // DMA with M > 1 rows staged (padded rows)
+  bool GM = false;   // k_rows_gm: group-major items, several units per workgroup
 };
 
 // Items each k_rows wave keeps in flight (the one being computed included),
@@ -1436,6 +1590,24 @@ Launch launch_for(int out_f, int G, int M) {
       const long long u2 = (long long)tiles * 2;
       l.P = (int)std::max<long long>(1, std::min(OUT == OUT_SWIGLU ? u2 / 2 : u2, (long long)cus));
       return l;
+    }
+    if constexpr (FMT == 4 && (OUT == OUT_BF16 || OUT == OUT_F32 || OUT == OUT_RES)) {
+      // Otherwise, several units per workgroup: group-major items, each
+      // activation group fetched once per workgroup (k_rows_gm). Measured on
+      // MI355X, gate|up at M = 16: 24.2 against 28.1 us for the per-item
+      // loads; at M = 9 the staged rows above stay faster (23.7 against 24.1).
+      const long long u2 = (long long)tiles * 2;
+      const long long pg = std::min<long long>(u2, cus);
+      if (mode != 1 && mode != 2 && mode != 4 && mode != 5 && u2 / pg >= kGmMinU &&
+          (u2 + pg - 1) / pg <= kGmMaxU) {
+        l.GM = true;
+        l.S = 2;
+        l.W = 8;
+        l.DMA = kGmD;
+        l.XL = false;
+        l.P = (int)pg;
+        return l;
+      }
     }
     int S = l.S;
     const int dd = (mode == 1 && tD >= 2 && tD <= 4 && !(OUT == OUT_ARGMAX && S == 4)) ? tD : 2;
@@ -1603,6 +1775,14 @@ void prepare_dma_one() {
     allow_lds<kern>(kLdsBytes - (int)at.sharedSizeBytes);
 }
 
+template <int OUT>
+void prepare_gm() {
+  constexpr auto kern = &k_rows_gm<OUT>;
+  hipFuncAttributes at{};
+  if (hipFuncGetAttributes(&at, reinterpret_cast<const void*>(kern)) == hipSuccess)
+    allow_lds<kern>(kLdsBytes - (int)at.sharedSizeBytes);
+}
+
 // Every LDS-DMA kernel the launch code can pick (launch_rows_dma).
 template <int OUT, int FMT>
 void prepare_dma_out() {
@@ -1631,6 +1811,9 @@ void prepare_dma_lds() {
     prepare_dec<OUT_RES>();
     prepare_dec<OUT_SWIGLU>();
     prepare_dec<OUT_NORM>();
+    prepare_gm<OUT_BF16>();
+    prepare_gm<OUT_F32>();
+    prepare_gm<OUT_RES>();
     prepare_dma_out<OUT_BF16, 4>();
     prepare_dma_out<OUT_F32, 4>();
     prepare_dma_out<OUT_ARGMAX, 4>();
@@ -1658,8 +1841,22 @@ void launch_rows_dma(const SkinnyArgs& a, int D, hipStream_t st) {
   }
 }
 
+template <int OUT>
+void launch_rows_gm(const SkinnyArgs& a, hipStream_t st) {
+  const int lds = 8 * gm_wave_units() * 16;
+  constexpr auto kern = &k_rows_gm<OUT>;
+  allow_lds<kern>(lds);
+  kern<<<a.P, 512, lds, st>>>(a);
+}
+
 template <int OUT, int FMT>
 void launch_rows(const SkinnyArgs& a, const Launch& l, hipStream_t st) {
+  if constexpr (FMT == 4 && (OUT == OUT_BF16 || OUT == OUT_F32 || OUT == OUT_RES)) {
+    if (l.GM) {
+      launch_rows_gm<OUT>(a, st);
+      return;
+    }
+  }
   if (l.DMA) {
     if constexpr (OUT != OUT_NORM) {
       if (l.XM) {   // M > 1 rows staged: 2 items per wave (launch_for)

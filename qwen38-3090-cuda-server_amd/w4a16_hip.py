@@ -419,8 +419,8 @@ def tune_decode(mode: int = 0, S: int = 0, W: int = 0, D: int = 0, P: int = 0) -
     """Tuning and test override of the skinny launches (qw4_tune_decode): mode 0
     the library's policy, 1 k_rows at M = 1 (D: LDS-DMA depth), 2 k_rows with
     register items (S, W: unit size and waves), 3 k_dec of shape S / W / D,
-    4 the policy without staging M > 1 activations in LDS; P forces k_dec's
-    workgroups (0 = policy)."""
+    4 the policy without staging M > 1 activations in LDS, 5 the policy without
+    the group-major M > 1 kernel; P forces k_dec's workgroups (0 = policy)."""
     _chk(lib().qw4_tune_decode(mode, S, W, D, P), "tune_decode")
 
 

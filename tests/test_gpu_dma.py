@@ -301,14 +301,16 @@ def test_dma_w8_verify(hip, scratch, M):
 # ------------------------------------------- M > 1 with the rows staged in LDS
 def _staged_vs_per_item(hip, run):
     """run() with the policy (the activation rows staged in LDS where they fit
-    and the workgroups own several units), with per-item activation loads
-    (qw4_tune_decode mode 4) and with register items (mode 2): every result
-    equal. The per-row sums run over the same groups in the same wave order in
-    every form, so any difference is a staging, padding or wait error."""
+    and the workgroups own several units; else, with 3 to 6 units per
+    workgroup, the group-major kernel k_rows_gm), with per-item activation
+    loads (qw4_tune_decode mode 4), with register items (mode 2) and with the
+    group-major kernel off (mode 5): every result equal. The per-row sums run
+    over the same groups in the same wave order in every form, so any
+    difference is a staging, padding, slot-reuse or wait error."""
     try:
         hip.tune_decode(0)
         want = run()
-        for mode in (4, 2):
+        for mode in (4, 2, 5):
             hip.tune_decode(mode)
             got = run()
             assert np.array_equal(got, want), mode
@@ -317,8 +319,11 @@ def _staged_vs_per_item(hip, run):
 
 
 # gate|up (544 tiles), a head-like 16384-row output, a short-K one; the 5120-row
-# output has fewer tiles than half the CUs and keeps the per-item loads
-STAGED = [(34816, 5120), (16384, 1024), (20480, 384), (5120, 4096)]
+# output has fewer tiles than half the CUs and keeps the per-item loads. Where
+# the rows do not fit the staging (M = 12 / 16 on gate|up, the 3- and
+# 6-units-per-workgroup shapes) the group-major kernel runs.
+STAGED = [(34816, 5120), (16384, 1024), (20480, 384), (5120, 4096), (24576, 5120),
+          (49152, 5120)]
 
 
 @pytest.mark.parametrize("M", [2, 9, 12, 16])
