@@ -115,21 +115,27 @@ struct G2Rsrc {
   __amdgpu_buffer_rsrc_t qw, sc, zr;
 };
 
+// part j < NH: the packed words of tile half j; part NH: the scales and zero
+// points; part -1: everything.
 template <int NH>
 __device__ __forceinline__ void g2_load_weights(WeightGroup<NH>& wg, const G2Rsrc& rs, int G,
-                                                int tile, int b0, int g, int lane) {
+                                                int tile, int b0, int g, int lane, int part = -1) {
   const int r = lane & 31, h = lane >> 5;
   const uint32_t blk = (uint32_t)tile * (uint32_t)G + (uint32_t)g;   // < 2^26
 #pragma unroll
   for (int j = 0; j < NH; ++j) {
     const int a16 = 8 * (b0 + j) + 2 * (r >> 3) + ((r >> 2) & 1);   // position % 16
     const int p = 16 * (r & 3) + a16;
+    if (part < 0 || part == j) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-      wg.q[j][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.qw, ((2 * s + h) * 64 + p) * 16,
-                                                         blk * 4096u, 0);
-    wg.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (4 * a16 + (r & 3)) * 2, blk * (uint32_t)kMetaBytes, 0);
-    wg.z[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.zr, a16 * 2, blk * 32u, 0);
+      for (int s = 0; s < 2; ++s)
+        wg.q[j][s] = __builtin_amdgcn_raw_buffer_load_b128(rs.qw, ((2 * s + h) * 64 + p) * 16,
+                                                           blk * 4096u, 0);
+    }
+    if (part < 0 || part == NH) {
+      wg.s[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.sc, (4 * a16 + (r & 3)) * 2, blk * (uint32_t)kMetaBytes, 0);
+      wg.z[j] = __builtin_amdgcn_raw_buffer_load_b16(rs.zr, a16 * 2, blk * 32u, 0);
+    }
   }
 }
 
@@ -247,18 +253,19 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
     __syncthreads();
     const int sb = (g - g0) & 1;
     const u32x4* buf = lds[sb] + (32 * mw + r) * 16;
-    // Group g + 1's weights now; its activation rows spread evenly over the
-    // first Sp::ACTSTEPS k-steps below, so that the 64 KiB the workgroup writes
-    // into LDS per group do not arrive in one burst on top of the first steps'
-    // operand reads (8 waves: steps 0-3, 4% faster than one burst and 1.5%
-    // than one load per step; 4 waves: all 8 steps, equal to steps 0-3).
+    // Group g + 1's activation rows spread evenly over the first Sp::ACTSTEPS
+    // k-steps below, so that the 64 KiB the workgroup writes into LDS per
+    // group do not arrive in one burst on top of the first steps' operand
+    // reads (8 waves: steps 0-3, 4% faster than one burst and 1.5% than one
+    // load per step; 4 waves: all 8 steps, equal to steps 0-3); its weights
+    // in k-steps kWStep.. kWStep + NH (0.5-0.8% faster than all at the
+    // group's start, where they delay its first MFMA).
     // Past the segment's last group the loads go through zero-length
     // resources: they fetch nothing (out-of-range buffer loads return zeros)
     // and need no branch, which would split the k-step schedule below.
     const bool more = g + 1 < g1;
     const __amdgpu_buffer_rsrc_t actn = more ? act : act_none;
     const G2Rsrc rsn = more ? rs : rs_none;
-    g2_load_weights(nxt, rsn, a.G, ltile, b0, g + 1, lane);
     float sf[NH], cf[NH];
 #pragma unroll
     for (int j = 0; j < NH; ++j) {
@@ -279,6 +286,9 @@ __device__ __forceinline__ void g2_segment(const GemmArgs& a, const G2Rsrc& rs,
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int cu = u & 1, nu = cu ^ 1;
+      constexpr int kWStep = 4;
+      if (u >= kWStep && u <= kWStep + NH)
+        g2_load_weights(nxt, rsn, a.G, ltile, b0, g + 1, lane, u - kWStep);
       if (u < Sp::ACTSTEPS) {
 #pragma unroll
         for (int i = 0; i < Sp::ACT / Sp::ACTSTEPS; ++i)
